@@ -1,0 +1,136 @@
+/* C ABI of the MI355X (gfx950) routed-expert MoE block.
+ *
+ * Plain device pointers, sizes and a hipStream_t passed as void*. No entry point
+ * allocates device memory or synchronises with the host: callers pass a workspace of
+ * moe_*_workspace_bytes(...) bytes, so every call can be captured in a HIP graph.
+ * All tensors are contiguous row-major. bf16 tensors are passed as raw 16-bit words.
+ * fp8 weights are OCP e4m3fn bytes with one fp32 scale per output row.
+ *
+ * Return value: 0 on success; MOE_EINVAL for an unsupported shape or argument (the
+ * reference's supported() predicates return False for these, engine/fast/moe_prefill.py:529-543);
+ * MOE_EHIP when a launch fails. moe_last_error() gives the message of the calling
+ * thread's last failure.
+ *
+ * Shapes: T tokens, H hidden, E experts, k experts per token, I expert intermediate,
+ * IS shared-expert intermediate. Expert weights follow Transformers' Qwen3_5MoeExperts
+ * (modeling_qwen3_5_moe.py:721-731): gate_up [E, 2I, H] (rows 0..I-1 gate, I..2I-1 up),
+ * down [E, H, I].
+ */
+#ifndef MOE_MI355X_H
+#define MOE_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MOE_OK 0
+#define MOE_EINVAL 1
+#define MOE_EHIP 2
+
+/* Weight element types. */
+#define MOE_WEIGHTS_BF16 0
+#define MOE_WEIGHTS_FP8_E4M3 1
+
+/* How the routing weight multiplies an expert's bf16 output before the fp32 sum over k.
+ * MOE_ROUND_PRODUCT: bf16(y * w), as Transformers' batched_mm (the decode path,
+ *   engine/experts.py:99-100 -> transformers/integrations/moe.py:165-171, and
+ *   engine/fast/kernels.py:163).
+ * MOE_EXACT_PRODUCT: y * w exact in fp32, as the padded / sorted / grouped prefill paths
+ *   (engine/experts.py:53-57,86-90; engine/fast/moe_prefill.py:580-582). */
+#define MOE_ROUND_PRODUCT 1
+#define MOE_EXACT_PRODUCT 2
+
+int moe_abi_version(void);
+const char* moe_last_error(void);
+
+/* Rows of the tile table's token tiles used by the fused entry points. */
+int moe_tile_rows(void);
+
+/* Tile-table capacity for T tokens: ceil(T*k/bm) + min(E, T*k) (+ ceil(T/bm) shared tiles). */
+int moe_max_tiles(int T, int k, int E, int bm, int has_shared);
+
+/* Router logits (a1). Replaces the router F.linear of
+ * modeling_qwen3_5_moe.py:768-769 / engine/fast/model.py:1159 and the packed
+ * router|shared-gate GEMV of engine/fast/fused.py:745-746 + mfma.py:90-119.
+ * w_pack [n_pack, H] bf16: rows 0..E-1 the router, row E the shared-expert gate
+ * (shared_expert_gate.weight), the rest zero; n_pack a multiple of 16.
+ * logits [T, n_pack] = bf16(x . w_pack^T). */
+int moe_router_logits(const void* x, int T, int H, const void* w_pack, int n_pack, void* logits,
+                      void* stream);
+
+/* Softmax / top-k / renormalise (a2). Replaces prefill_kernels.route
+ * (engine/fast/prefill_kernels.py:650-663, kernel :194-219) and the router of
+ * modeling_qwen3_5_moe.py:770-774. Ties go to the lower expert index.
+ * logits [T, ld] bf16 (first E columns used); idx64 [T, k]; w_out [T, k] bf16;
+ * counts [E] int32 (optional, incremented: pass zeros). */
+int moe_route_topk(const void* logits, long long ld, int T, int E, int k, long long* idx64,
+                   void* w_out, int* counts, void* stream);
+
+/* Count / stable sort / tile table (a3). Replaces the argsort + bincount of
+ * engine/experts.py:71-80, moe_prefill.py:562-566 and build_tiles
+ * (moe_prefill.py:509-521, _tiles_one_kernel :128-154).
+ * idx64 [T, k]; counts [E], offsets [E] (exclusive cumsum), order [T*k] = stable argsort
+ * of the flat ids; table [3*max_tiles + 1] in the layout of moe_prefill.py:92-126
+ * (plus shared tiles (E, T*k + j*bm, T*k + T) after the routed ones when has_shared).
+ * scratch: moe_sort_scratch_bytes(T*k, E) bytes. */
+size_t moe_sort_scratch_bytes(int P, int E);
+int moe_sort(const long long* idx64, int T, int k, int E, int bm, int has_shared, int* counts,
+             int* offsets, int* order, int* table, int max_tiles, void* scratch, void* stream);
+
+/* Grouped expert gate_up (a4 / a8): act[r] = bf16(bf16(silu(bf16 g)) * bf16 u) for sorted
+ * row r of pair order[r] (token order[r] / k). Replaces moe_prefill._gate_up_kernel
+ * (engine/fast/moe_prefill.py:156-211) and kernels._moe_gate_up_kernel (kernels.py:88-125).
+ * act [T*k, I] bf16. gu_scale [E, 2I] fp32 for fp8 weights, else null. */
+int moe_grouped_gate_up(const void* x, int T, int H, int E, int k, int I, const void* gate_up,
+                        const float* gu_scale, int wdtype, const int* order, const int* table,
+                        int max_tiles, void* act, void* stream);
+
+/* Grouped expert down (a5 / a9): y[order[r]] = bf16(act[r] . Wd[e]) at each pair's own row.
+ * Replaces moe_prefill._down_kernel / _down_stream_kernel (moe_prefill.py:212-319).
+ * y [T*k, H] bf16. dn_scale [E, H] fp32 for fp8 weights, else null. */
+int moe_grouped_down(const void* act, int T, int H, int E, int k, int I, const void* down,
+                     const float* dn_scale, int wdtype, const int* order, const int* table,
+                     int max_tiles, void* y, void* stream);
+
+/* Combine (a7 / a10): out[t] = bf16(bf16(sum_j term(y[t*k+j], w[t,j]))
+ *   + bf16(bf16(sigmoid(seg[t])) * ysh[t])) (+ residual). Replaces
+ * prefill_kernels._moe_combine_kernel (engine/fast/prefill_kernels.py:253-273) and the
+ * weighted sums of transformers/integrations/moe.py:165-174 / engine/experts.py:53-57.
+ * ysh / seg / residual may be null. mode: MOE_ROUND_PRODUCT or MOE_EXACT_PRODUCT. */
+int moe_combine(const void* y, const void* w, int T, int H, int k, const void* ysh,
+                const void* seg, long long ld_seg, const void* residual, void* out, int mode,
+                void* stream);
+
+/* Routed experts only (surface 1): the experts_forward(self, hidden_states, top_k_index,
+ * top_k_weights) of engine/experts.py:93-102 (batched_mm for T <= 16, padded bmm above).
+ * out [T, H] bf16. */
+size_t moe_experts_workspace_bytes(int T, int H, int E, int k, int I);
+int moe_experts_forward(const void* x, int T, int H, int E, int k, int I,
+                        const long long* top_k_index, const void* top_k_weights,
+                        const void* gate_up, const float* gu_scale, const void* down,
+                        const float* dn_scale, int wdtype, int mode, void* out, void* workspace,
+                        size_t workspace_bytes, void* stream);
+
+/* Whole block (surface 2): router + top-k + routed experts + gated shared expert
+ * (+ residual). Replaces FastModel._moe (engine/fast/model.py:1139-1179),
+ * prefill_kernels.moe (prefill_kernels.py:676-742), FusedDecode._moe (fused.py:887-932)
+ * and Qwen3_5MoeSparseMoeBlock.forward (modeling_qwen3_5_moe.py:787-800).
+ * sh_gate / sh_up [IS, H], sh_down [H, IS] bf16. residual [T, H] or null.
+ * top_k_index [T, k] int64 / top_k_weights [T, k] bf16 / logits [T, n_pack] bf16 are
+ * optional outputs (null: kept in the workspace). */
+size_t moe_block_workspace_bytes(int T, int H, int E, int k, int I, int IS, int n_pack);
+int moe_block_forward(const void* x, int T, int H, int E, int k, int I, int IS,
+                      const void* w_pack, int n_pack, const void* gate_up, const float* gu_scale,
+                      const void* down, const float* dn_scale, int wdtype, const void* sh_gate,
+                      const void* sh_up, const void* sh_down, const void* residual, int mode,
+                      void* out, long long* top_k_index, void* top_k_weights, void* logits,
+                      void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MOE_MI355X_H */

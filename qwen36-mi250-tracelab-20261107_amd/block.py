@@ -1,0 +1,134 @@
+"""Block-level MoE (router + top-k + routed experts + gated shared expert) on MI355X.
+
+``moe(x, mlp, top_k)`` has the call surface of the reference's block-level MoE
+(``FastModel._moe`` engine/fast/model.py:1139-1179, ``prefill_kernels.moe``
+engine/fast/prefill_kernels.py:676-742): ``mlp`` is a Transformers
+``Qwen3_5MoeSparseMoeBlock`` (or any object with the same attributes: ``gate.weight``,
+``shared_expert.{gate,up,down}_proj.weight``, ``shared_expert_gate.weight``,
+``experts.{gate_up_proj,down_proj}``) and the result is the block's output [T, H].
+``moe(x, mlp, top_k, residual=r)`` returns ``r + MoE(x)`` rounded as
+``FusedDecode._moe`` (engine/fast/fused.py:887-932).
+
+Everything runs in one C-ABI call (``moe_block_forward``): router GEMV/GEMM, softmax /
+top-k, count + stable sort + tile table, grouped gate_up (routed experts and the shared
+expert in one launch), grouped down, combine. Rounding of the routing-weight products
+follows ``FastModel._moe``: bf16(w * y) for decode steps and for at most
+``DECODE_EXPERT_TOKENS`` tokens (the batched_mm path), exact fp32 products above.
+
+fp8-e4m3 experts: ``experts.gate_up_proj`` / ``down_proj`` of dtype float8_e4m3fn with
+per-output-row fp32 scales in ``experts.gate_up_scale`` [E, 2I] / ``experts.down_scale``
+[E, H] (see ``fp8.quantize_experts``).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from ._lib import check, ptr, stream_of
+from .ops import _need_cuda, expert_weight
+
+DECODE_EXPERT_TOKENS = 16  # engine/fast/model.py:48
+
+_PACK_ATTR = "_mi355x_router_pack"
+
+
+def pack_router(mlp) -> torch.Tensor:
+    """The router rows and the shared-expert gate row as one [n_pack, H] bf16 tensor
+    (rows 0..E-1 router, row E shared gate, zero rows up to a multiple of 16), built once
+    per block and cached on it (the packing engine/fast/fused.py:699-746 does for its
+    router|shared GEMV). Rebuilt when either source weight changes."""
+    router = mlp.gate.weight
+    seg = mlp.shared_expert_gate.weight
+    key = (router.data_ptr(), router._version, seg.data_ptr(), seg._version, router.device)
+    cached = getattr(mlp, _PACK_ATTR, None)
+    if cached is not None and cached[0] == key:
+        return cached[1]
+    experts, hidden = router.shape
+    n_pack = (experts + 1 + 15) // 16 * 16
+    pack = torch.zeros((n_pack, hidden), dtype=torch.bfloat16, device=router.device)
+    with torch.no_grad():
+        pack[:experts].copy_(router)
+        pack[experts].copy_(seg.reshape(-1))
+    setattr(mlp, _PACK_ATTR, (key, pack))
+    return pack
+
+
+def _expert_tensors(experts):
+    gu = experts.gate_up_proj
+    dn = experts.down_proj
+    gus = getattr(experts, "gate_up_scale", None)
+    dns = getattr(experts, "down_scale", None)
+    gu, gus, wd = expert_weight(gu.data if isinstance(gu, torch.nn.Parameter) else gu, gus, "gate_up")
+    dn, dns, wd2 = expert_weight(dn.data if isinstance(dn, torch.nn.Parameter) else dn, dns, "down")
+    if wd != wd2:
+        raise ValueError("gate_up_proj and down_proj must share one weight dtype")
+    if not (gu.is_contiguous() and dn.is_contiguous()):
+        raise ValueError("expert weights must be contiguous row-major")
+    return gu, gus, dn, dns, wd
+
+
+def supported(x: torch.Tensor, mlp, top_k: int) -> bool:
+    """Whether ``moe`` runs this block (engine/fast/prefill_kernels.py:666-673's role)."""
+    try:
+        gu, _, dn, _, _ = _expert_tensors(mlp.experts)
+    except ValueError:
+        return False
+    e, two_i, h = gu.shape
+    inter_s = mlp.shared_expert.gate_proj.weight.shape[0]
+    return (
+        x.dtype == torch.bfloat16
+        and x.device.type == "cuda"
+        and h % 32 == 0
+        and (two_i // 2) % 32 == 0
+        and inter_s % 32 == 0
+        and 1 <= top_k <= min(64, e)
+        and e <= 1024
+    )
+
+
+def moe(x: torch.Tensor, mlp, top_k: int, decode: bool = False,
+        residual: torch.Tensor | None = None, *, return_routing: bool = False):
+    """MoE(x) [T, H] bf16 for ``x`` [T, H] (or residual + MoE(x)). With ``return_routing``
+    also (top_k_index int64 [T, k], top_k_weights bf16 [T, k], router logits [T, n_pack])."""
+    shape = x.shape
+    x2 = x.reshape(-1, shape[-1])
+    _need_cuda(x2)
+    if x2.dtype != torch.bfloat16:
+        raise ValueError(f"x must be bfloat16 (got {x2.dtype})")
+    x2 = x2.contiguous()
+    tokens, hidden = x2.shape
+    gu, gus, dn, dns, wd = _expert_tensors(mlp.experts)
+    experts, two_i, _ = gu.shape
+    inter = two_i // 2
+    sh = mlp.shared_expert
+    sg = sh.gate_proj.weight
+    su = sh.up_proj.weight
+    sd = sh.down_proj.weight
+    inter_s = sg.shape[0]
+    for w, name in ((sg, "shared gate"), (su, "shared up"), (sd, "shared down")):
+        if w.dtype != torch.bfloat16 or not w.is_contiguous():
+            raise ValueError(f"{name} weight must be contiguous bfloat16")
+    pack = pack_router(mlp)
+    n_pack = pack.shape[0]
+    if residual is not None:
+        residual = residual.reshape(tokens, hidden).to(torch.bfloat16).contiguous()
+    round_products = decode or tokens <= DECODE_EXPERT_TOKENS
+    mode = _lib.ROUND_PRODUCT if round_products else _lib.EXACT_PRODUCT
+    out = torch.empty((tokens, hidden), dtype=torch.bfloat16, device=x2.device)
+    idx = torch.empty((tokens, top_k), dtype=torch.long, device=x2.device) if return_routing else None
+    wts = torch.empty((tokens, top_k), dtype=torch.bfloat16, device=x2.device) if return_routing else None
+    logits = (torch.empty((tokens, n_pack), dtype=torch.bfloat16, device=x2.device)
+              if return_routing else None)
+    if tokens:
+        lib = _lib.load()
+        nbytes = lib.moe_block_workspace_bytes(tokens, hidden, experts, top_k, inter, inter_s, n_pack)
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=x2.device)
+        check(lib.moe_block_forward(
+            ptr(x2), tokens, hidden, experts, top_k, inter, inter_s, ptr(pack), n_pack, ptr(gu),
+            ptr(gus), ptr(dn), ptr(dns), wd, ptr(sg), ptr(su), ptr(sd), ptr(residual), mode,
+            ptr(out), ptr(idx), ptr(wts), ptr(logits), ptr(ws), nbytes, stream_of(x2)), "moe block")
+    out = out.reshape(shape)
+    if return_routing:
+        return out, idx, wts, logits
+    return out

@@ -1,0 +1,456 @@
+// extern "C" entry points of libmoe_mi355x.so (declared in include/moe_mi355x.h).
+// Validation, workspace carving and the launch sequence of the MoE block; the kernels
+// live in route_sort.hip, stream_gemm.hip and combine.hip.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <string>
+
+#include "../../include/moe_mi355x.h"
+#include "stream_gemm.h"
+
+namespace moe {
+hipError_t launch_route(const uint16_t* logits, long long ld, int T, int E, int k, long long* idx64,
+                        int* idx32, uint16_t* w_out, int* counts, hipStream_t s);
+hipError_t launch_route_sort(const uint16_t* logits, long long ld, const int* ids32_in,
+                             const long long* ids64_in, int T, int E, int k, int bm, int has_shared,
+                             long long* idx64, int* idx32, uint16_t* w_out, int* counts,
+                             int* offsets, int* order, int* table, int MT, int* scratch,
+                             hipStream_t s);
+size_t sort_scratch_bytes(int P, int E);
+hipError_t launch_combine(const uint16_t* y, const uint16_t* w, int k, const uint16_t* ysh,
+                          const uint16_t* seg, long long ld_seg, const uint16_t* res, uint16_t* out,
+                          int T, int H, int round_w, hipStream_t s);
+}  // namespace moe
+
+using namespace moe;
+
+namespace {
+
+constexpr int kBM = 64;  // token rows per tile of the streaming GEMM (16 * TOKB)
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+int hip_check(hipError_t e, const char* what) {
+  if (e == hipSuccess) return MOE_OK;
+  return fail(MOE_EHIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+#define CHECK_ARG(cond, ...) \
+  do {                       \
+    if (!(cond)) return fail(MOE_EINVAL, __VA_ARGS__); \
+  } while (0)
+
+#define HIP_TRY(expr, what)                     \
+  do {                                          \
+    int rc_ = hip_check((expr), what);          \
+    if (rc_ != MOE_OK) return rc_;              \
+  } while (0)
+
+size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
+
+// Sequential carve of a caller-provided workspace.
+struct Carver {
+  char* base;
+  size_t off = 0;
+  template <class Tp>
+  Tp* take(size_t count) {
+    Tp* p = base ? reinterpret_cast<Tp*>(base + off) : nullptr;
+    off += align256(count * sizeof(Tp));
+    return p;
+  }
+};
+
+int max_tiles_of(int T, int k, int E, int bm, int has_shared) {
+  long long P = (long long)T * k;
+  long long mt = (P + bm - 1) / bm + (P < E ? P : E);
+  if (has_shared) mt += (T + bm - 1) / bm;
+  return (int)mt;
+}
+
+int check_experts_shape(int T, int H, int E, int k, int I) {
+  CHECK_ARG(T >= 0, "T must be >= 0 (got %d)", T);
+  CHECK_ARG(E >= 1 && E <= 1024, "experts must be in [1, 1024] (got %d)", E);
+  CHECK_ARG(k >= 1 && k <= 64 && k <= E, "top_k must be in [1, min(64, E)] (got %d)", k);
+  CHECK_ARG(H >= 32 && H % 32 == 0, "hidden must be a positive multiple of 32 (got %d)", H);
+  CHECK_ARG(I >= 32 && I % 32 == 0, "intermediate must be a positive multiple of 32 (got %d)", I);
+  CHECK_ARG((long long)T * k < (1LL << 30), "too many pairs");
+  return MOE_OK;
+}
+
+GemmOperand gate_up_operand(const void* gate_up, const float* scale, int H, int I, const void* in,
+                            void* act) {
+  GemmOperand o{};
+  o.w = gate_up;
+  o.estride = 2LL * I * H;
+  o.up_off = (long long)I * H;
+  o.ldw = H;
+  o.scale = scale;
+  o.sstride = 2LL * I;
+  o.s_up_off = I;
+  o.K = H;
+  o.N = I;
+  o.in = static_cast<const uint16_t*>(in);
+  o.ld_in = H;
+  o.out = static_cast<uint16_t*>(act);
+  o.ld_out = I;
+  o.in_map = 1;
+  o.out_map = 0;
+  return o;
+}
+
+GemmOperand down_operand(const void* down, const float* scale, int H, int I, const void* act,
+                         void* y) {
+  GemmOperand o{};
+  o.w = down;
+  o.estride = (long long)H * I;
+  o.ldw = I;
+  o.scale = scale;
+  o.sstride = H;
+  o.K = I;
+  o.N = H;
+  o.in = static_cast<const uint16_t*>(act);
+  o.ld_in = I;
+  o.out = static_cast<uint16_t*>(y);
+  o.ld_out = H;
+  o.in_map = 0;
+  o.out_map = 1;
+  return o;
+}
+
+int run_gate_up(const void* x, int T, int H, int E, int k, int I, const void* gate_up,
+                const float* gu_scale, int wdtype, const void* sh_gate, const void* sh_up, int IS,
+                const int* order, const int* table, int MT, void* act, void* act_sh,
+                hipStream_t s) {
+  GemmArgs a{};
+  a.op[0] = gate_up_operand(gate_up, gu_scale, H, I, x, act);
+  if (sh_gate) {
+    GemmOperand& v = a.op[1];
+    v.w = sh_gate;
+    v.up_off = (long long)((intptr_t)sh_up - (intptr_t)sh_gate) / 2;
+    v.ldw = H;
+    v.K = H;
+    v.N = IS;
+    v.in = static_cast<const uint16_t*>(x);
+    v.ld_in = H;
+    v.out = static_cast<uint16_t*>(act_sh);
+    v.ld_out = IS;
+  } else {
+    a.op[1] = a.op[0];
+    a.op[1].N = 0;
+  }
+  a.table = table;
+  a.MT = MT;
+  a.order = order;
+  a.topk = k;
+  a.P = T * k;
+  a.E = E;
+  a.T = T;
+  hipError_t err = launch_stream_gemm(kModeSwiglu, kRoleGateUp, wdtype == MOE_WEIGHTS_FP8_E4M3, a,
+                                      MT, s);
+  if (err == hipErrorInvalidValue)
+    return fail(MOE_EINVAL, "gate_up: no kernel configuration for H=%d I=%d IS=%d", H, I, IS);
+  return hip_check(err, "gate_up launch");
+}
+
+int run_down(const void* act, int T, int H, int E, int k, int I, const void* down,
+             const float* dn_scale, int wdtype, const void* sh_down, int IS, const void* act_sh,
+             const int* order, const int* table, int MT, void* y, void* y_sh, hipStream_t s) {
+  GemmArgs a{};
+  a.op[0] = down_operand(down, dn_scale, H, I, act, y);
+  if (sh_down) {
+    GemmOperand& v = a.op[1];
+    v.w = sh_down;
+    v.ldw = IS;
+    v.K = IS;
+    v.N = H;
+    v.in = static_cast<const uint16_t*>(act_sh);
+    v.ld_in = IS;
+    v.out = static_cast<uint16_t*>(y_sh);
+    v.ld_out = H;
+  } else {
+    a.op[1] = a.op[0];
+    a.op[1].N = 0;
+  }
+  a.table = table;
+  a.MT = MT;
+  a.order = order;
+  a.topk = k;
+  a.P = T * k;
+  a.E = E;
+  a.T = T;
+  hipError_t err = launch_stream_gemm(kModePlain, kRoleDown, wdtype == MOE_WEIGHTS_FP8_E4M3, a,
+                                      MT, s);
+  if (err == hipErrorInvalidValue)
+    return fail(MOE_EINVAL, "down: no kernel configuration for H=%d I=%d IS=%d", H, I, IS);
+  return hip_check(err, "down launch");
+}
+
+}  // namespace
+
+extern "C" {
+
+int moe_abi_version(void) { return 1; }
+
+const char* moe_last_error(void) { return g_err.c_str(); }
+
+int moe_tile_rows(void) { return kBM; }
+
+int moe_max_tiles(int T, int k, int E, int bm, int has_shared) {
+  if (T < 0 || k < 1 || E < 1 || bm < 1) return 0;
+  return max_tiles_of(T, k, E, bm, has_shared);
+}
+
+int moe_router_logits(const void* x, int T, int H, const void* w_pack, int n_pack, void* logits,
+                      void* stream) {
+  CHECK_ARG(T >= 0, "T must be >= 0");
+  CHECK_ARG(H >= 32 && H % 32 == 0, "hidden must be a positive multiple of 32 (got %d)", H);
+  CHECK_ARG(n_pack >= 16 && n_pack % 16 == 0, "n_pack must be a positive multiple of 16 (got %d)",
+            n_pack);
+  CHECK_ARG(x && w_pack && logits, "null pointer");
+  if (T == 0) return MOE_OK;
+  GemmArgs a{};
+  GemmOperand& v = a.op[1];
+  v.w = w_pack;
+  v.ldw = H;
+  v.K = H;
+  v.N = n_pack;
+  v.in = static_cast<const uint16_t*>(x);
+  v.ld_in = H;
+  v.out = static_cast<uint16_t*>(logits);
+  v.ld_out = n_pack;
+  a.op[0] = v;
+  a.op[0].N = 0;
+  a.table = nullptr;
+  a.P = 0;
+  a.E = 0;
+  a.T = T;
+  int mt = (T + kBM - 1) / kBM;
+  hipError_t err = launch_stream_gemm(kModePlain, kRoleRouter, false, a, mt, (hipStream_t)stream);
+  if (err == hipErrorInvalidValue) return fail(MOE_EINVAL, "router: no configuration for H=%d", H);
+  return hip_check(err, "router launch");
+}
+
+int moe_route_topk(const void* logits, long long ld, int T, int E, int k, long long* idx64,
+                   void* w_out, int* counts, void* stream) {
+  CHECK_ARG(T >= 0, "T must be >= 0");
+  CHECK_ARG(E >= 1 && E <= 1024, "experts must be in [1, 1024] (got %d)", E);
+  CHECK_ARG(k >= 1 && k <= 64 && k <= E, "top_k must be in [1, min(64, E)] (got %d)", k);
+  CHECK_ARG(ld >= E, "logits row stride %lld < experts %d", ld, E);
+  CHECK_ARG(logits && idx64 && w_out, "null pointer");
+  return hip_check(launch_route(static_cast<const uint16_t*>(logits), ld, T, E, k, idx64, nullptr,
+                                static_cast<uint16_t*>(w_out), counts, (hipStream_t)stream),
+                   "route launch");
+}
+
+size_t moe_sort_scratch_bytes(int P, int E) { return sort_scratch_bytes(P, E); }
+
+int moe_sort(const long long* idx64, int T, int k, int E, int bm, int has_shared, int* counts,
+             int* offsets, int* order, int* table, int max_tiles, void* scratch, void* stream) {
+  CHECK_ARG(T >= 0 && k >= 1 && E >= 1 && E <= 1024, "bad T/k/E (%d, %d, %d)", T, k, E);
+  CHECK_ARG(bm >= 1, "bm must be >= 1");
+  CHECK_ARG(max_tiles >= max_tiles_of(T, k, E, bm, has_shared), "max_tiles %d < %d", max_tiles,
+            max_tiles_of(T, k, E, bm, has_shared));
+  CHECK_ARG(idx64 && order && table, "null pointer");
+  CHECK_ARG(sort_scratch_bytes(T * k, E) == 0 || scratch, "scratch required");
+  return hip_check(launch_route_sort(nullptr, 0, nullptr, idx64, T, E, k, bm, has_shared, nullptr,
+                                     nullptr, nullptr, counts, offsets, order, table, max_tiles,
+                                     static_cast<int*>(scratch), (hipStream_t)stream),
+                   "sort launch");
+}
+
+int moe_grouped_gate_up(const void* x, int T, int H, int E, int k, int I, const void* gate_up,
+                        const float* gu_scale, int wdtype, const int* order, const int* table,
+                        int max_tiles, void* act, void* stream) {
+  int rc = check_experts_shape(T, H, E, k, I);
+  if (rc) return rc;
+  CHECK_ARG(wdtype == MOE_WEIGHTS_BF16 || (wdtype == MOE_WEIGHTS_FP8_E4M3 && gu_scale),
+            "bad weight dtype / missing scales");
+  if (T == 0) return MOE_OK;
+  return run_gate_up(x, T, H, E, k, I, gate_up, gu_scale, wdtype, nullptr, nullptr, 0, order,
+                     table, max_tiles, act, nullptr, (hipStream_t)stream);
+}
+
+int moe_grouped_down(const void* act, int T, int H, int E, int k, int I, const void* down,
+                     const float* dn_scale, int wdtype, const int* order, const int* table,
+                     int max_tiles, void* y, void* stream) {
+  int rc = check_experts_shape(T, H, E, k, I);
+  if (rc) return rc;
+  CHECK_ARG(wdtype == MOE_WEIGHTS_BF16 || (wdtype == MOE_WEIGHTS_FP8_E4M3 && dn_scale),
+            "bad weight dtype / missing scales");
+  if (T == 0) return MOE_OK;
+  return run_down(act, T, H, E, k, I, down, dn_scale, wdtype, nullptr, 0, nullptr, order, table,
+                  max_tiles, y, nullptr, (hipStream_t)stream);
+}
+
+int moe_combine(const void* y, const void* w, int T, int H, int k, const void* ysh,
+                const void* seg, long long ld_seg, const void* residual, void* out, int mode,
+                void* stream) {
+  CHECK_ARG(T >= 0 && H % 8 == 0 && H > 0 && k >= 1, "bad combine shape");
+  CHECK_ARG(mode == MOE_ROUND_PRODUCT || mode == MOE_EXACT_PRODUCT, "bad mode %d", mode);
+  CHECK_ARG(!ysh || seg, "shared output needs the gate logits");
+  return hip_check(launch_combine(static_cast<const uint16_t*>(y), static_cast<const uint16_t*>(w),
+                                  k, static_cast<const uint16_t*>(ysh),
+                                  static_cast<const uint16_t*>(seg), ld_seg,
+                                  static_cast<const uint16_t*>(residual),
+                                  static_cast<uint16_t*>(out), T, H, mode == MOE_ROUND_PRODUCT,
+                                  (hipStream_t)stream),
+                   "combine launch");
+}
+
+// ------------------------------------------------------------------ routed experts only
+
+namespace {
+struct ExpertsWs {
+  int *idx32, *counts, *offsets, *order, *table, *scratch;
+  uint16_t *act, *y;
+  size_t bytes;
+  int MT;
+};
+ExpertsWs carve_experts(void* base, int T, int H, int E, int k, int I) {
+  Carver c{static_cast<char*>(base)};
+  ExpertsWs w{};
+  const int P = T * k;
+  w.MT = max_tiles_of(T, k, E, kBM, 0);
+  w.counts = c.take<int>(E);
+  w.offsets = c.take<int>(E);
+  w.order = c.take<int>(P);
+  w.table = c.take<int>(3 * (size_t)w.MT + 1);
+  w.scratch = c.take<int>(sort_scratch_bytes(P, E) / sizeof(int) + 1);
+  w.act = c.take<uint16_t>((size_t)P * I);
+  w.y = c.take<uint16_t>((size_t)P * H);
+  w.bytes = c.off;
+  return w;
+}
+}  // namespace
+
+size_t moe_experts_workspace_bytes(int T, int H, int E, int k, int I) {
+  if (T < 0 || k < 1 || E < 1) return 0;
+  return carve_experts(nullptr, T, H, E, k, I).bytes;
+}
+
+int moe_experts_forward(const void* x, int T, int H, int E, int k, int I,
+                        const long long* top_k_index, const void* top_k_weights,
+                        const void* gate_up, const float* gu_scale, const void* down,
+                        const float* dn_scale, int wdtype, int mode, void* out, void* workspace,
+                        size_t workspace_bytes, void* stream) {
+  int rc = check_experts_shape(T, H, E, k, I);
+  if (rc) return rc;
+  CHECK_ARG(mode == MOE_ROUND_PRODUCT || mode == MOE_EXACT_PRODUCT, "bad mode %d", mode);
+  CHECK_ARG(wdtype == MOE_WEIGHTS_BF16 ||
+                (wdtype == MOE_WEIGHTS_FP8_E4M3 && gu_scale && dn_scale),
+            "bad weight dtype / missing scales");
+  CHECK_ARG(x && top_k_index && top_k_weights && gate_up && down && out, "null pointer");
+  if (T == 0) return MOE_OK;
+  ExpertsWs w = carve_experts(workspace, T, H, E, k, I);
+  CHECK_ARG(workspace && workspace_bytes >= w.bytes, "workspace too small: %zu < %zu",
+            workspace_bytes, w.bytes);
+  hipStream_t s = (hipStream_t)stream;
+  HIP_TRY(launch_route_sort(nullptr, 0, nullptr, top_k_index, T, E, k, kBM, 0, nullptr, nullptr,
+                            nullptr, w.counts, w.offsets, w.order, w.table, w.MT, w.scratch, s),
+          "sort launch");
+  rc = run_gate_up(x, T, H, E, k, I, gate_up, gu_scale, wdtype, nullptr, nullptr, 0, w.order,
+                   w.table, w.MT, w.act, nullptr, s);
+  if (rc) return rc;
+  rc = run_down(w.act, T, H, E, k, I, down, dn_scale, wdtype, nullptr, 0, nullptr, w.order, w.table,
+                w.MT, w.y, nullptr, s);
+  if (rc) return rc;
+  return hip_check(launch_combine(w.y, static_cast<const uint16_t*>(top_k_weights), k, nullptr,
+                                  nullptr, 0, nullptr, static_cast<uint16_t*>(out), T, H,
+                                  mode == MOE_ROUND_PRODUCT, s),
+                   "combine launch");
+}
+
+// ------------------------------------------------------------------------ whole block
+
+namespace {
+struct BlockWs {
+  uint16_t* logits;
+  long long* idx64;
+  int* idx32;
+  uint16_t* w;
+  int *counts, *offsets, *order, *table, *scratch;
+  uint16_t *act, *act_sh, *y, *y_sh;
+  size_t bytes;
+  int MT;
+};
+BlockWs carve_block(void* base, int T, int H, int E, int k, int I, int IS, int n_pack) {
+  Carver c{static_cast<char*>(base)};
+  BlockWs w{};
+  const int P = T * k;
+  w.MT = max_tiles_of(T, k, E, kBM, 1);
+  w.logits = c.take<uint16_t>((size_t)T * n_pack);
+  w.idx64 = c.take<long long>(P);
+  w.idx32 = c.take<int>(P);
+  w.w = c.take<uint16_t>(P);
+  w.counts = c.take<int>(E);
+  w.offsets = c.take<int>(E);
+  w.order = c.take<int>(P);
+  w.table = c.take<int>(3 * (size_t)w.MT + 1);
+  w.scratch = c.take<int>(sort_scratch_bytes(P, E) / sizeof(int) + 1);
+  w.act = c.take<uint16_t>((size_t)P * I);
+  w.act_sh = c.take<uint16_t>((size_t)T * IS);
+  w.y = c.take<uint16_t>((size_t)P * H);
+  w.y_sh = c.take<uint16_t>((size_t)T * H);
+  w.bytes = c.off;
+  return w;
+}
+}  // namespace
+
+size_t moe_block_workspace_bytes(int T, int H, int E, int k, int I, int IS, int n_pack) {
+  if (T < 0 || k < 1 || E < 1) return 0;
+  return carve_block(nullptr, T, H, E, k, I, IS, n_pack).bytes;
+}
+
+int moe_block_forward(const void* x, int T, int H, int E, int k, int I, int IS,
+                      const void* w_pack, int n_pack, const void* gate_up, const float* gu_scale,
+                      const void* down, const float* dn_scale, int wdtype, const void* sh_gate,
+                      const void* sh_up, const void* sh_down, const void* residual, int mode,
+                      void* out, long long* top_k_index, void* top_k_weights, void* logits,
+                      void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = check_experts_shape(T, H, E, k, I);
+  if (rc) return rc;
+  CHECK_ARG(IS >= 32 && IS % 32 == 0, "shared intermediate must be a multiple of 32 (got %d)", IS);
+  CHECK_ARG(n_pack >= E + 1 && n_pack % 16 == 0, "n_pack must be >= E + 1 and a multiple of 16");
+  CHECK_ARG(mode == MOE_ROUND_PRODUCT || mode == MOE_EXACT_PRODUCT, "bad mode %d", mode);
+  CHECK_ARG(wdtype == MOE_WEIGHTS_BF16 ||
+                (wdtype == MOE_WEIGHTS_FP8_E4M3 && gu_scale && dn_scale),
+            "bad weight dtype / missing scales");
+  CHECK_ARG(x && w_pack && gate_up && down && sh_gate && sh_up && sh_down && out, "null pointer");
+  CHECK_ARG((((intptr_t)sh_up - (intptr_t)sh_gate) & 1) == 0, "misaligned shared weights");
+  if (T == 0) return MOE_OK;
+  BlockWs w = carve_block(workspace, T, H, E, k, I, IS, n_pack);
+  CHECK_ARG(workspace && workspace_bytes >= w.bytes, "workspace too small: %zu < %zu",
+            workspace_bytes, w.bytes);
+  hipStream_t s = (hipStream_t)stream;
+  uint16_t* lg = logits ? static_cast<uint16_t*>(logits) : w.logits;
+  long long* i64 = top_k_index ? top_k_index : w.idx64;
+  uint16_t* wt = top_k_weights ? static_cast<uint16_t*>(top_k_weights) : w.w;
+  rc = moe_router_logits(x, T, H, w_pack, n_pack, lg, stream);
+  if (rc) return rc;
+  HIP_TRY(launch_route_sort(lg, n_pack, nullptr, nullptr, T, E, k, kBM, 1, i64, w.idx32, wt,
+                            w.counts, w.offsets, w.order, w.table, w.MT, w.scratch, s),
+          "route/sort launch");
+  rc = run_gate_up(x, T, H, E, k, I, gate_up, gu_scale, wdtype, sh_gate, sh_up, IS, w.order,
+                   w.table, w.MT, w.act, w.act_sh, s);
+  if (rc) return rc;
+  rc = run_down(w.act, T, H, E, k, I, down, dn_scale, wdtype, sh_down, IS, w.act_sh, w.order,
+                w.table, w.MT, w.y, w.y_sh, s);
+  if (rc) return rc;
+  return hip_check(launch_combine(w.y, wt, k, w.y_sh, lg + E, n_pack,
+                                  static_cast<const uint16_t*>(residual),
+                                  static_cast<uint16_t*>(out), T, H, mode == MOE_ROUND_PRODUCT, s),
+                   "combine launch");
+}
+
+}  // extern "C"

@@ -1,0 +1,46 @@
+// Arguments of the expert-grouped weight-streaming GEMM (stream_gemm.hip).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace moe {
+
+constexpr int kModePlain = 0;   // out = bf16(acc * scale)
+constexpr int kModeSwiglu = 1;  // out = bf16(bf16(silu(bf16 g)) * bf16 u), gate/up row pairs
+
+constexpr int kRoleRouter = 0;
+constexpr int kRoleGateUp = 1;
+constexpr int kRoleDown = 2;
+
+// One weight family: the routed experts (op[0]) or the virtual expert id E (op[1],
+// the shared expert or the router), whose rows map 1:1 to tokens (row r -> token r - P).
+struct GemmOperand {
+  const void* w;        // expert 0, output row 0 (SWIGLU: gate row 0); bf16 or fp8 elements
+  long long estride;    // elements between experts
+  long long up_off;     // SWIGLU: elements from gate row n to up row n
+  long long ldw;        // elements per weight row
+  const float* scale;   // per-output-row fp32 scales (fp8) or null
+  long long sstride;    // scales per expert
+  long long s_up_off;   // SWIGLU: scale index of up row 0
+  int K, N;             // reduction length; output rows (SWIGLU: gate rows)
+  const uint16_t* in;   // B operand rows (bf16)
+  long long ld_in;
+  uint16_t* out;        // bf16 output rows
+  long long ld_out;
+  int in_map;           // routed: 1 -> B row = token of pair order[r]; 0 -> B row = r
+  int out_map;          // routed: 1 -> out row = pair order[r]; 0 -> out row = r
+};
+
+struct GemmArgs {
+  GemmOperand op[2];
+  const int* table;  // tile table, or null: virtual-expert tiles over rows P .. P + T
+  int MT;            // table capacity (max tiles)
+  const int* order;  // sorted row -> pair
+  int topk, P, E, T;
+  int nrb;           // weight-row blocks per tile (set by the launcher)
+};
+
+hipError_t launch_stream_gemm(int mode, int role, bool fp8, const GemmArgs& a, int max_tiles,
+                              hipStream_t st);
+
+}  // namespace moe

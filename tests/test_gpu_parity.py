@@ -1,0 +1,242 @@
+"""Parity of the gfx950 kernels (through the C ABI) against the CPU oracle.
+
+Bar: expert indices, counts, offsets, permutation and tile table bit-exact; bf16 values
+within the reference tests' tolerance (max-abs <= 2e-2 * max(1, |ref|max), the bound of
+engine tests/test_moe_prefill.py:56,80) of the bf16-rounding oracle, and within
+max-abs 2e-2 / mean-rel 5e-3 of the fp32 oracle (the north star's bf16 bar).
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle import moe_oracle as orc
+from tests.helpers import BF16, max_abs, mean_rel, router_rows, routing
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-2
+
+
+def _say(*a):
+    print(*a, flush=True)
+
+
+# ----------------------------------------------------------------------------- routing
+
+
+@pytest.mark.parametrize("E,k", [(256, 8), (16, 4), (8, 2), (64, 8), (128, 1)])
+@pytest.mark.parametrize("seed", [0, 1])
+def test_route_bitexact(pkg, dev, E, k, seed):
+    _say("route", E, k, seed)
+    g = torch.Generator().manual_seed(100 + seed)
+    logits = torch.cat([router_rows(64, E, seed), torch.randn(64, E, generator=g).to(BF16)])
+    w, i, counts = pkg.ops.route(logits.to(dev), k)
+    torch.cuda.synchronize()
+    ref_w, ref_i = orc.route(logits, k)
+    assert torch.equal(i.cpu(), ref_i)
+    # weights: the renormalising sum's order may differ by one fp32 ulp -> one bf16 ulp at most
+    diff = (w.float().cpu() - ref_w.float()).abs()
+    assert (diff <= ref_w.float().abs() * 2.0 ** -7 + 1e-30).all()
+    assert torch.equal(counts.cpu(), torch.bincount(ref_i.reshape(-1), minlength=E).int())
+
+
+def test_route_bruteforce_small(pkg, dev):
+    logits = router_rows(16, 8, 7)
+    _, i, _ = pkg.ops.route(logits.to(dev), 3)
+    torch.cuda.synchronize()
+    assert torch.equal(i.cpu(), orc.route_bruteforce(logits, 3))
+
+
+# -------------------------------------------------------------------------------- sort
+
+
+SORT_CASES = [(1, 256, 8), (4, 16, 4), (64, 256, 8), (75, 16, 4), (300, 16, 4), (513, 256, 8),
+              (1000, 256, 8), (2049, 64, 2)]
+
+
+@pytest.mark.parametrize("T,E,k", SORT_CASES)
+@pytest.mark.parametrize("mode", ["uniform", "skewed", "sparse", "one"])
+@pytest.mark.parametrize("shared", [False, True])
+def test_sort_bitexact(pkg, dev, T, E, k, mode, shared):
+    _say("sort", T, E, k, mode, shared)
+    g = torch.Generator().manual_seed(T * 7 + E)
+    idx, _ = routing(T, E, k, mode, g)
+    bm = 64
+    sp = pkg.ops.sort_pairs(idx.to(dev), E, bm=bm, shared=shared)
+    torch.cuda.synchronize()
+    counts, offsets, order, tiles = orc.sort_pairs(idx, E, bm, tokens=T, shared=shared)
+    assert torch.equal(sp.counts.cpu(), torch.from_numpy(counts))
+    assert torch.equal(sp.offsets.cpu(), torch.from_numpy(offsets))
+    assert torch.equal(sp.order.cpu(), torch.from_numpy(order))
+    assert torch.equal(sp.order.cpu().long(), torch.argsort(idx.reshape(-1), stable=True))
+    mt = sp.max_tiles
+    assert mt == orc.max_tiles(T, k, E, bm, shared)
+    tab = sp.table.cpu()
+    n = int(tab[3 * mt])
+    assert n == len(tiles)
+    got = [(int(tab[t]), int(tab[mt + t]), int(tab[2 * mt + t])) for t in range(n)]
+    assert got == tiles
+
+
+def test_sort_deterministic(pkg, dev):
+    g = torch.Generator().manual_seed(5)
+    idx, _ = routing(3000, 256, 8, "skewed", g)
+    a = pkg.ops.sort_pairs(idx.to(dev), 256)
+    b = pkg.ops.sort_pairs(idx.to(dev), 256)
+    torch.cuda.synchronize()
+    assert torch.equal(a.order, b.order) and torch.equal(a.table, b.table)
+
+
+# ------------------------------------------------------------------------- experts
+
+
+class _Experts(torch.nn.Module):
+    """engine tests/test_moe_prefill.py:14-27's experts holder (weights * 0.1)."""
+
+    def __init__(self, e, h, i, seed=0):
+        super().__init__()
+        g = torch.Generator().manual_seed(seed)
+        self.num_experts = e
+        self.gate_up_proj = torch.randn(e, 2 * i, h, generator=g).mul(0.1).to(BF16)
+        self.down_proj = torch.randn(e, h, i, generator=g).mul(0.1).to(BF16)
+        self.act_fn = torch.nn.functional.silu
+
+
+@pytest.mark.parametrize("n", [1, 4, 16, 17, 40, 300])
+@pytest.mark.parametrize("mode", ["uniform", "skewed", "sparse", "one"])
+@pytest.mark.parametrize("shape", [(16, 128, 64, 4), (8, 64, 32, 2), (32, 256, 128, 8)])
+def test_experts_forward_matches_oracle(pkg, dev, n, mode, shape):
+    e, h, i, k = shape
+    _say("experts", n, mode, shape)
+    m = _Experts(e, h, i, seed=n)
+    g = torch.Generator().manual_seed(n + 1)
+    x = torch.randn(n, h, generator=g).to(BF16)
+    idx, w = routing(n, e, k, mode, g)
+    gpu = _Experts(e, h, i, seed=n)
+    gpu.gate_up_proj, gpu.down_proj = m.gate_up_proj.to(dev), m.down_proj.to(dev)
+    got = pkg.experts.experts_forward(gpu, x.to(dev), idx.to(dev), w.to(dev))
+    again = pkg.experts.experts_forward(gpu, x.to(dev), idx.to(dev), w.to(dev))
+    torch.cuda.synchronize()
+    ref = orc.experts_forward(x, idx, w, m.gate_up_proj, m.down_proj)
+    scale = max(1.0, ref.float().abs().max().item())
+    assert got.dtype == BF16 and got.shape == ref.shape
+    assert max_abs(got, ref) <= TOL * scale
+    assert torch.equal(got, again), "not deterministic"
+
+
+@pytest.mark.parametrize("n", [3, 40])
+def test_grouped_stages_match_oracle(pkg, dev, n):
+    """gate_up -> act (sorted rows) and down -> y (pair rows) separately."""
+    e, h, i, k = 16, 128, 64, 4
+    m = _Experts(e, h, i, seed=3)
+    g = torch.Generator().manual_seed(n)
+    x = torch.randn(n, h, generator=g).to(BF16)
+    idx, w = routing(n, e, k, "uniform", g)
+    gu, dn = m.gate_up_proj.to(dev), m.down_proj.to(dev)
+    sp = pkg.ops.sort_pairs(idx.to(dev), e)
+    act = pkg.ops.grouped_gate_up(x.to(dev), k, gu, sp)
+    y = pkg.ops.grouped_down(act, n, k, dn, sp)
+    out_r = pkg.ops.combine(y, w.to(dev), round_products=True)
+    out_e = pkg.ops.combine(y, w.to(dev), round_products=False)
+    torch.cuda.synchronize()
+    ref_act, ref_y = orc.pair_outputs_bf16(x, idx, m.gate_up_proj, m.down_proj)
+    order = sp.order.cpu().long()
+    assert max_abs(act.cpu(), ref_act[order]) <= TOL * max(1.0, ref_act.float().abs().max().item())
+    assert max_abs(y.cpu(), ref_y) <= TOL * max(1.0, ref_y.float().abs().max().item())
+    ref_r = orc.batched_mm_experts(x, idx, w, m.gate_up_proj, m.down_proj)
+    ref_e = orc.sorted_experts(x, idx, w, m.gate_up_proj, m.down_proj)
+    assert max_abs(out_r, ref_r) <= TOL and max_abs(out_e, ref_e) <= TOL
+    # combine itself on identical pair outputs: exact fp32 product path is exact in fp32
+    y_ref_bits = ref_y.to(dev)
+    out_c = pkg.ops.combine(y_ref_bits, w.to(dev), round_products=False).cpu()
+    want = (ref_y.float() * w.reshape(-1, 1).float()).view(n, k, -1).sum(1).to(BF16)
+    assert max_abs(out_c, want) <= 2.0 ** -8 * max(1.0, want.float().abs().max().item())
+
+
+# -------------------------------------------------------------------------------- block
+
+
+def _gpu_mlp(w, dev):
+    import __graft_entry__
+
+    return __graft_entry__._mlp_from_weights(w, dev)
+
+
+@pytest.mark.parametrize("T", [1, 4, 17, 64])
+def test_block_c1_shape(pkg, dev, T):
+    """C1 layer (H256, E16, k4, I=IS=128) against both oracles."""
+    _say("block c1", T)
+    H, E, K, I = 256, 16, 4, 128
+    w = orc.make_weights(H, E, I, I, seed=0)
+    g = torch.Generator().manual_seed(T)
+    x = torch.randn(T, H, generator=g).to(BF16)
+    out, idx, wts, logits = pkg.block.moe(x.to(dev), _gpu_mlp(w, dev), K, return_routing=True)
+    torch.cuda.synchronize()
+    lg = logits.cpu()[:, :E]
+    ref_w, ref_i = orc.route(lg, K)
+    assert torch.equal(idx.cpu(), ref_i)
+    ref_lg = torch.nn.functional.linear(x, w["router"])
+    assert max_abs(lg, ref_lg) <= 2.0 ** -7 * max(1.0, ref_lg.float().abs().max().item())
+    ref, _, _, _ = orc.block_bf16(x, w, K)
+    f32 = orc.block_fp32(x, w, ref_i, logits=lg)
+    _say(" vs bf16 oracle", max_abs(out, ref), " vs fp32", max_abs(out, f32), mean_rel(out, f32))
+    assert max_abs(out, f32) <= 2e-2 and mean_rel(out, f32) <= 5e-3
+
+
+def _full_weights(dev, seed=0, zipf=False):
+    H, E, I = 2048, 256, 512
+    g = torch.Generator(device=dev).manual_seed(seed)
+
+    def rnd(*shape):
+        return (torch.randn(*shape, generator=g, device=dev) * 0.02).to(BF16)
+
+    w = {
+        "router": rnd(E, H), "gate_up": rnd(E, 2 * I, H), "down": rnd(E, H, I),
+        "sh_gate": rnd(I, H), "sh_up": rnd(I, H), "sh_down": rnd(H, I), "sh_gate_w": rnd(1, H),
+    }
+    v = None
+    if zipf:
+        r, v = orc.zipf_router(w["router"].cpu(), s=1.1, mu=4.0, seed=seed)
+        w["router"] = r.to(dev)
+    return w, v
+
+
+@pytest.fixture(scope="module")
+def full_layer(dev):
+    return _full_weights(dev, seed=0)
+
+
+@pytest.mark.parametrize("T", [1, 8, 64])
+def test_block_full_shape(pkg, dev, full_layer, T):
+    """C2/C3-shaped layer (H2048, E256, k8, I=IS=512): routing bit-exact given the logits,
+    values vs the fp32 oracle."""
+    _say("block full", T)
+    w, _ = full_layer
+    g = torch.Generator().manual_seed(T)
+    x = torch.randn(T, 2048, generator=g).to(BF16)
+    out, idx, wts, logits = pkg.block.moe(x.to(dev), _gpu_mlp(w, dev), 8, return_routing=True)
+    torch.cuda.synchronize()
+    lg = logits.cpu()[:, :256]
+    ref_w, ref_i = orc.route(lg, 8)
+    assert torch.equal(idx.cpu(), ref_i)
+    ref_lg = torch.nn.functional.linear(x, w["router"].cpu())
+    assert max_abs(lg, ref_lg) <= 2.0 ** -7 * max(1.0, ref_lg.float().abs().max().item())
+    f32 = orc.block_fp32(x, w, ref_i, logits=lg)
+    _say(" vs fp32", max_abs(out, f32), mean_rel(out, f32))
+    assert max_abs(out, f32) <= 2e-2 and mean_rel(out, f32) <= 5e-3
+
+
+def test_block_residual(pkg, dev):
+    H, E, K, I = 256, 16, 4, 128
+    w = orc.make_weights(H, E, I, I, seed=1)
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(5, H, generator=g).to(BF16)
+    r = torch.randn(5, H, generator=g).to(BF16)
+    mlp = _gpu_mlp(w, dev)
+    a = pkg.block.moe(x.to(dev), mlp, K)
+    b = pkg.block.moe(x.to(dev), mlp, K, residual=r.to(dev))
+    torch.cuda.synchronize()
+    want = (r.float() + a.cpu().float()).to(BF16)
+    assert torch.equal(b.cpu(), want)

@@ -1,0 +1,85 @@
+"""Host-side checks that need no GPU: the C-ABI library loads and exports every symbol
+include/moe_mi355x.h declares, argument validation, workspace and tile-count formulas."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from oracle import moe_oracle as orc
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def _declared_symbols():
+    text = (ROOT / "include" / "moe_mi355x.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\**\s+\**(moe_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_declares_entry_points():
+    names = _declared_symbols()
+    assert "moe_block_forward" in names and "moe_route_topk" in names and len(names) >= 14
+
+
+def test_library_exports_every_declared_symbol(pkg):
+    lib = pkg._lib.load()
+    for name in _declared_symbols():
+        assert hasattr(lib, name), name
+        assert name in pkg._lib.SIGNATURES, f"{name} has no ctypes signature"
+    assert set(pkg._lib.SIGNATURES) == set(_declared_symbols())
+    assert lib.moe_abi_version() == 1
+
+
+@pytest.mark.parametrize("T,k,E,bm,sh", [(1, 8, 256, 64, 1), (64, 8, 256, 64, 1),
+                                          (4096, 8, 256, 64, 0), (0, 4, 16, 64, 1), (3, 2, 4, 2, 1)])
+def test_max_tiles_formula(pkg, T, k, E, bm, sh):
+    assert pkg._lib.load().moe_max_tiles(T, k, E, bm, sh) == orc.max_tiles(T, k, E, bm, bool(sh))
+
+
+def test_workspace_grows_with_tokens(pkg):
+    lib = pkg._lib.load()
+    a = lib.moe_block_workspace_bytes(1, 2048, 256, 8, 512, 512, 272)
+    b = lib.moe_block_workspace_bytes(64, 2048, 256, 8, 512, 512, 272)
+    assert 0 < a < b
+    # the pair outputs [P, H] and activations [P, I] dominate
+    assert b >= 64 * 8 * (2048 + 512) * 2
+    assert lib.moe_experts_workspace_bytes(16, 128, 16, 4, 64) > 0
+
+
+def test_invalid_arguments_raise_before_any_launch(pkg):
+    lib = pkg._lib.load()
+    rc = lib.moe_route_topk(None, 16, 4, 16, 99, None, None, None, None)
+    assert rc == pkg._lib.MOE_EINVAL
+    assert b"top_k" in lib.moe_last_error()
+    rc = lib.moe_experts_forward(None, 4, 100, 16, 4, 64, None, None, None, None, None, None, 0, 1,
+                                 None, None, 0, None)
+    assert rc == pkg._lib.MOE_EINVAL and b"hidden" in lib.moe_last_error()
+    rc = lib.moe_combine(None, None, 1, 2048, 8, None, None, 0, None, None, 7, None)
+    assert rc == pkg._lib.MOE_EINVAL
+
+
+def test_cpu_tensors_fail_loudly(pkg):
+    x = torch.zeros(2, 64, dtype=torch.bfloat16)
+    with pytest.raises(pkg.MoeLibraryError, match="no CPU path"):
+        pkg.ops.route(x, 2)
+
+
+def test_supported_predicate(pkg):
+    x = torch.zeros(2, 64, dtype=torch.bfloat16)
+    gu = torch.zeros(4, 64, 64, dtype=torch.bfloat16)
+    dn = torch.zeros(4, 64, 32, dtype=torch.bfloat16)
+    assert not pkg.ops.supported(x, gu, dn)  # CPU tensor
+
+
+def test_fp8_quantize_matches_oracle(pkg):
+    g = torch.Generator().manual_seed(0)
+    w = (torch.randn(3, 32, 64, generator=g) * 0.02).to(torch.bfloat16)
+    q, s = pkg.fp8.quantize_rows(w)
+    q2, s2 = orc.quantize_rows(w)
+    assert torch.equal(q.view(torch.uint8), q2.view(torch.uint8)) and torch.equal(s, s2)
+    assert q.dtype == torch.float8_e4m3fn and s.shape == (3, 32)
