@@ -1,0 +1,315 @@
+"""Benchmark of the MI355X MoE block (the BASELINE.json metric) on one GPU.
+
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs c2,c3,c4,c5] [--no-cpu]
+
+A step is one MoE layer call (router -> top-k -> sort -> grouped gate_up -> grouped down
+-> combine) on one batch of synthetic tokens with that layer's inputs already in HBM.
+Layers cycle through L distinct weight sets (more bytes than L2 + MALL) so every step
+streams its experts from HBM. Steps are captured in a HIP graph of L layer calls and
+replayed; K is rounded up to a multiple of L and the JSON reports the K timed.
+
+The headline workload is C2 (decode batch 1, H2048 E256 top-8 + shared, I=IS=512, bf16):
+``value`` = microseconds per layer (lower is better). The same line carries the C3
+(batch 64, Zipf(1.1) routing), C4 (4096-token prefill) and C5 (40-layer fp8 stack at
+batch 32) results, the roofline of the dominant kernel (the grouped gate_up launch, timed
+with HIP events on the stream it runs on) and the CPU baseline (the CPU torch oracle of
+the reference path, timed on this host's cores on a bounded sample).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+H, E, K_TOP, I, IS = 2048, 256, 8, 512, 512
+SEEDS = {"c2": 1000, "c3": 2000, "c4": 3000, "c5": 4000}
+METRIC = json.loads((ROOT / "BASELINE.json").read_text())["metric"] if (ROOT / "BASELINE.json").exists() \
+    else "MoE layer us + achieved HBM TB/s (% peak), E=256 top-8 h=2048, batch 1/64"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+class NS:
+    def __init__(self, **kw):
+        self.__dict__.update(kw)
+
+
+def make_layer(torch, dev, seed, zipf=False, fp8=False):
+    """One full-shape layer's weights on ``dev`` (bf16 ~ N(0, 0.02); fp8 per-row if asked)."""
+    g = torch.Generator(device=dev).manual_seed(seed)
+
+    def rnd(*shape):
+        return (torch.randn(*shape, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+
+    router = rnd(E, H)
+    v = None
+    if zipf:
+        from oracle import moe_oracle as orc  # noqa: PLC0415 - synthetic-input construction only
+
+        r, v = orc.zipf_router(router.cpu(), s=1.1, mu=4.0, seed=seed)
+        router = r.to(dev)
+        v = v.to(dev)
+    gu, dn = rnd(E, 2 * I, H), rnd(E, H, I)
+    experts = NS(gate_up_proj=gu, down_proj=dn, num_experts=E)
+    if fp8:
+        pkg = load_pkg()
+        q, s = pkg.fp8.quantize_rows(gu)
+        experts.gate_up_proj, experts.gate_up_scale = q, s
+        del gu
+        q, s = pkg.fp8.quantize_rows(dn)
+        experts.down_proj, experts.down_scale = q, s
+        del dn
+    mlp = NS(
+        gate=NS(weight=router),
+        shared_expert=NS(gate_proj=NS(weight=rnd(IS, H)), up_proj=NS(weight=rnd(IS, H)),
+                         down_proj=NS(weight=rnd(H, IS))),
+        shared_expert_gate=NS(weight=rnd(1, H)),
+        experts=experts,
+    )
+    return mlp, v
+
+
+_PKG = None
+
+
+def load_pkg():
+    global _PKG
+    if _PKG is None:
+        import __graft_entry__
+
+        _PKG = __graft_entry__.load_package()
+    return _PKG
+
+
+def layer_bytes(D, T, fp8=False):
+    """Algorithmic HBM bytes of one layer: each distinct expert's weights once, the shared
+    expert, the router | shared-gate rows, activations in and out."""
+    per_expert = 3 * I * H * (1 if fp8 else 2) + (3 * I * 4 if fp8 else 0)  # + fp32 row scales
+    weights = D * per_expert + 3 * IS * H * 2 + (E + 1) * H * 2
+    acts = T * H * 2 * 2 + T * K_TOP * (I + H) * 2 * 2
+    return weights + acts
+
+
+def gate_up_bytes(D, T, fp8=False):
+    """Algorithmic bytes of the grouped gate_up launch (routed + shared)."""
+    per_expert = 2 * I * H * (1 if fp8 else 2) + (2 * I * 4 if fp8 else 0)
+    return D * per_expert + 2 * IS * H * 2 + T * H * 2 + (T * K_TOP * I + T * IS) * 2
+
+
+def capture(torch, fn):
+    """A HIP graph of ``fn()`` on a side stream (torch's capture)."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()  # warm the caching allocator outside the capture
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    torch.cuda.synchronize()
+    return g
+
+
+def time_graph(torch, g, reps, warmup):
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        g.replay()
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop)  # ms
+
+
+def run_config(torch, dev, name, T, layers, steps, warmup, zipf=False, fp8=False):
+    """Times ``steps`` layer calls of config ``name``; returns a result dict."""
+    pkg = load_pkg()
+    t0 = time.time()
+    mlps, xs = [], []
+    for li in range(layers):
+        mlp, v = make_layer(torch, dev, seed=SEEDS[name] + li, zipf=zipf, fp8=fp8)
+        g = torch.Generator(device=dev).manual_seed(li + 7)
+        x = torch.randn(T, H, generator=g, device=dev)
+        if v is not None:
+            x = x + 4.0 * v[None, :]
+        mlps.append(mlp)
+        xs.append(x.to(torch.bfloat16))
+        pkg.block.pack_router(mlp)
+    torch.cuda.synchronize()
+    log(f"[{name}] {layers} layers ready in {time.time() - t0:.1f}s")
+
+    # routing statistics (outside the timed region)
+    Ds, ok = [], True
+    for mlp, x in zip(mlps, xs):
+        out, idx, _, _ = pkg.block.moe(x, mlp, K_TOP, return_routing=True)
+        Ds.append(int(torch.unique(idx).numel()))
+        ok = ok and bool(torch.isfinite(out.float()).all())
+    torch.cuda.synchronize()
+    D = sum(Ds) / len(Ds)
+
+    def layer_pass():
+        for mlp, x in zip(mlps, xs):
+            pkg.block.moe(x, mlp, K_TOP, decode=T <= 64)
+
+    graph = capture(torch, layer_pass)
+    reps = max(1, -(-steps // layers))
+    wreps = max(1, -(-warmup // layers))
+    ms = time_graph(torch, graph, reps, wreps)
+    nsteps = reps * layers
+    us_layer = ms * 1000.0 / nsteps
+    lbytes = sum(layer_bytes(d, T, fp8) for d in Ds) / len(Ds)
+    res = {
+        "T": T, "layers": layers, "steps": nsteps, "us_per_layer": round(us_layer, 3),
+        "tokens_per_s": round(T / (us_layer * 1e-6), 1), "distinct_experts": round(D, 2),
+        "layer_bytes": int(lbytes), "layer_TBps": round(lbytes / (us_layer * 1e-6) / 1e12, 3),
+        "layer_hbm_frac": round(lbytes / (us_layer * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+        "finite": ok, "weights": "fp8_e4m3" if fp8 else "bf16",
+    }
+    if T >= 1024:
+        flops = 2 * T * K_TOP * 3 * I * H + 2 * T * 3 * IS * H + 2 * T * (E + 1) * H
+        res["tflops"] = round(flops / (us_layer * 1e-6) / 1e12, 2)
+        res["mfma_frac_bf16"] = round(flops / (us_layer * 1e-6) / 1e12 / BF16_PEAK_TFLOPS, 4)
+    del graph
+
+    # the dominant kernel alone: the grouped gate_up launch of each layer (routed + shared)
+    sps = []
+    for mlp, x in zip(mlps, xs):
+        logits = pkg.ops.router_logits(x, pkg.block.pack_router(mlp))
+        _, idx, _ = pkg.ops.route(logits, K_TOP, experts=E)
+        sps.append(pkg.ops.sort_pairs(idx, E, shared=True))
+    torch.cuda.synchronize()
+
+    def gate_up_pass():
+        for mlp, x, sp in zip(mlps, xs, sps):
+            ex = mlp.experts
+            pkg.ops.grouped_gate_up(x, K_TOP, ex.gate_up_proj, sp,
+                                    scale=getattr(ex, "gate_up_scale", None),
+                                    shared=(mlp.shared_expert.gate_proj.weight,
+                                            mlp.shared_expert.up_proj.weight))
+
+    graph = capture(torch, gate_up_pass)
+    ms = time_graph(torch, graph, reps, wreps)
+    us_k = ms * 1000.0 / nsteps
+    kbytes = sum(gate_up_bytes(d, T, fp8) for d in Ds) / len(Ds)
+    res["gate_up_us"] = round(us_k, 3)
+    res["gate_up_bytes"] = int(kbytes)
+    res["gate_up_GBps"] = round(kbytes / (us_k * 1e-6) / 1e9, 1)
+    del graph, sps, mlps, xs
+    torch.cuda.empty_cache()
+    log(f"[{name}] {json.dumps(res)}")
+    return res
+
+
+def cpu_baseline(torch, seconds):
+    """The CPU torch restatement of the reference path (oracle.block_bf16: Transformers
+    block with batched_mm experts, engine/experts.py) on C2, timed on this host."""
+    from oracle import moe_oracle as orc
+
+    w = orc.make_weights(H, E, I, IS, seed=0)
+    g = torch.Generator().manual_seed(1)
+    xs = [torch.randn(1, H, generator=g).to(torch.bfloat16) for _ in range(8)]
+    orc.block_bf16(xs[0], w, K_TOP)  # warm
+    n, t0 = 0, time.perf_counter()
+    times = []
+    while time.perf_counter() - t0 < seconds:
+        t1 = time.perf_counter()
+        orc.block_bf16(xs[n % len(xs)], w, K_TOP)
+        times.append(time.perf_counter() - t1)
+        n += 1
+    times.sort()
+    med = times[len(times) // 2]
+    return {
+        "value": round(med * 1e6, 1), "unit": "us/layer", "cores": torch.get_num_threads(),
+        "affinity_cores": len(os.sched_getaffinity(0)), "kind": "port",
+        "sample": f"C2 decode batch 1, {n} layer calls of the bf16 CPU torch path "
+                  f"(oracle.block_bf16 = Transformers block + batched_mm experts) over "
+                  f"{seconds:.0f}s, median",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=32)
+    ap.add_argument("--configs", default="c2,c3,c4,c5")
+    ap.add_argument("--layers", type=int, default=16)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (the MoE block runs "
+              "on one GPU with no TP/EP exchange); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP device", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda:0")
+    pkg = load_pkg()
+    pkg._lib.load()
+    cfgs = [c.strip() for c in args.configs.split(",") if c.strip()]
+    results = {}
+    if "c2" in cfgs:
+        results["c2"] = run_config(torch, dev, "c2", 1, args.layers, args.steps, args.warmup)
+    if "c3" in cfgs:
+        results["c3"] = run_config(torch, dev, "c3", 64, args.layers, args.steps, args.warmup,
+                                   zipf=True)
+    if "c4" in cfgs:
+        results["c4"] = run_config(torch, dev, "c4", 4096, 4, max(8, args.steps // 32),
+                                   max(4, args.warmup // 8))
+    if "c5" in cfgs:
+        results["c5"] = run_config(torch, dev, "c5", 32, 40, max(40, args.steps // 40 * 40),
+                                   40, fp8=True)
+    head = results.get("c2") or next(iter(results.values()))
+    cpu = None if args.no_cpu else cpu_baseline(torch, args.cpu_seconds)
+    kbytes, kus = head["gate_up_bytes"], head["gate_up_us"]
+    achieved = kbytes / (kus * 1e-6) / 1e9
+    line = {
+        "metric": METRIC,
+        "value": head["us_per_layer"],
+        "unit": "us/layer",
+        "n_gpus": 1,
+        "steps": head["steps"],
+        "warmup": args.warmup,
+        "ms_per_step": round(head["us_per_layer"] / 1000.0, 6),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (weights ~N(0,0.02) random-init, activations ~N(0,1))",
+        "config": {"workload": "C2 MoE layer decode batch 1: H2048 E256 top-8 + shared, "
+                               "I=IS=512, bf16, 16 distinct layers cycled",
+                   "tokens": head["T"], "parallelism": "single GPU"},
+        "hbm_TBps": head["layer_TBps"],
+        "hbm_frac": head["layer_hbm_frac"],
+        "tokens_per_s": head["tokens_per_s"],
+        "roofline": {"bound": "hbm", "kernel": "grouped gate_up (k_stream_gemm SWIGLU)",
+                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "bytes_per_launch": kbytes, "us_per_launch": kus},
+        "cpu_baseline": cpu,
+        "configs": results,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

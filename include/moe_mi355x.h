@@ -83,17 +83,22 @@ int moe_sort(const long long* idx64, int T, int k, int E, int bm, int has_shared
 /* Grouped expert gate_up (a4 / a8): act[r] = bf16(bf16(silu(bf16 g)) * bf16 u) for sorted
  * row r of pair order[r] (token order[r] / k). Replaces moe_prefill._gate_up_kernel
  * (engine/fast/moe_prefill.py:156-211) and kernels._moe_gate_up_kernel (kernels.py:88-125).
- * act [T*k, I] bf16. gu_scale [E, 2I] fp32 for fp8 weights, else null. */
+ * act [T*k, I] bf16. gu_scale [E, 2I] fp32 for fp8 weights, else null.
+ * With sh_gate / sh_up [IS, H] (and a table built with has_shared) the same launch also
+ * computes the shared expert's act_sh [T, IS] (a6; prefill_kernels.py:232-251). */
 int moe_grouped_gate_up(const void* x, int T, int H, int E, int k, int I, const void* gate_up,
                         const float* gu_scale, int wdtype, const int* order, const int* table,
-                        int max_tiles, void* act, void* stream);
+                        int max_tiles, void* act, const void* sh_gate, const void* sh_up, int IS,
+                        void* act_sh, void* stream);
 
 /* Grouped expert down (a5 / a9): y[order[r]] = bf16(act[r] . Wd[e]) at each pair's own row.
  * Replaces moe_prefill._down_kernel / _down_stream_kernel (moe_prefill.py:212-319).
- * y [T*k, H] bf16. dn_scale [E, H] fp32 for fp8 weights, else null. */
+ * y [T*k, H] bf16. dn_scale [E, H] fp32 for fp8 weights, else null.
+ * With sh_down [H, IS] the same launch also writes y_sh [T, H] = bf16(act_sh . Wsd). */
 int moe_grouped_down(const void* act, int T, int H, int E, int k, int I, const void* down,
                      const float* dn_scale, int wdtype, const int* order, const int* table,
-                     int max_tiles, void* y, void* stream);
+                     int max_tiles, void* y, const void* sh_down, int IS, const void* act_sh,
+                     void* y_sh, void* stream);
 
 /* Combine (a7 / a10): out[t] = bf16(bf16(sum_j term(y[t*k+j], w[t,j]))
  *   + bf16(bf16(sigmoid(seg[t])) * ysh[t])) (+ residual). Replaces

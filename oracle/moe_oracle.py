@@ -229,6 +229,37 @@ def block_bf16(x, w, top_k, decode=False):
     return out, top_i, top_w, logits
 
 
+def block_bf16_routed(x, w, top_i, top_w, logits, decode=False):
+    """``block_bf16`` for a given routing (top_i, bf16 top_w) and bf16 router logits
+    [T, >E] (column E = the shared-expert gate logit): lets a test feed the GPU's own
+    routing and a compacted set of experts."""
+    shared = shared_expert(x, w["sh_gate"], w["sh_up"], w["sh_down"])
+    gu, dn = w["gate_up"], w["down"]
+    if decode or x.shape[0] <= DECODE_EXPERT_TOKENS:
+        routed = batched_mm_experts(x, top_i, top_w, gu, dn)
+    else:
+        routed = sorted_experts(x, top_i, top_w, gu, dn)
+    gate = torch.sigmoid(logits[:, -1:]) if logits is not None else torch.sigmoid(
+        F.linear(x, w["sh_gate_w"]))
+    return routed + gate * shared
+
+
+def compact_experts(w, top_i):
+    """(w', top_i') with only the experts ``top_i`` uses, copied to the CPU, and the
+    indices renumbered into them (for checking full-size layers whose experts live on
+    the GPU)."""
+    uniq = torch.unique(top_i.cpu())
+    remap = torch.full((int(uniq.max()) + 1,), -1, dtype=torch.long)
+    remap[uniq] = torch.arange(uniq.numel())
+    out = {k: (v.cpu() if k not in ("gate_up", "down", "gate_up_scale", "down_scale") else v)
+           for k, v in w.items()}
+    dev_idx = uniq.to(w["gate_up"].device)
+    for k in ("gate_up", "down", "gate_up_scale", "down_scale"):
+        if k in w:
+            out[k] = w[k][dev_idx].cpu()
+    return out, remap[top_i.cpu()]
+
+
 def block_fp32(x, w, top_i, top_w=None, logits=None):
     """The block in fp32 for a given routing (bit-exact indices are a separate contract):
     every matmul and activation in fp32 from the bf16 weights, renormalised fp32 routing

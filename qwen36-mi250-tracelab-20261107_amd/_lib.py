@@ -38,8 +38,10 @@ SIGNATURES: dict[str, tuple] = {
     "moe_route_topk": (_I, [_P, _LL, _I, _I, _I, _P, _P, _P, _P]),
     "moe_sort_scratch_bytes": (_SZ, [_I, _I]),
     "moe_sort": (_I, [_P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _I, _P, _P]),
-    "moe_grouped_gate_up": (_I, [_P, _I, _I, _I, _I, _I, _P, _P, _I, _P, _P, _I, _P, _P]),
-    "moe_grouped_down": (_I, [_P, _I, _I, _I, _I, _I, _P, _P, _I, _P, _P, _I, _P, _P]),
+    "moe_grouped_gate_up": (
+        _I, [_P, _I, _I, _I, _I, _I, _P, _P, _I, _P, _P, _I, _P, _P, _P, _I, _P, _P]),
+    "moe_grouped_down": (
+        _I, [_P, _I, _I, _I, _I, _I, _P, _P, _I, _P, _P, _I, _P, _P, _I, _P, _P, _P]),
     "moe_combine": (_I, [_P, _P, _I, _I, _I, _P, _P, _LL, _P, _P, _I, _P]),
     "moe_experts_workspace_bytes": (_SZ, [_I, _I, _I, _I, _I]),
     "moe_experts_forward": (

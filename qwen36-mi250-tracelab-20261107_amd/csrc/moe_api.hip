@@ -134,6 +134,7 @@ int run_gate_up(const void* x, int T, int H, int E, int k, int I, const void* ga
                 hipStream_t s) {
   GemmArgs a{};
   a.op[0] = gate_up_operand(gate_up, gu_scale, H, I, x, act);
+  a.op[0].fp8 = wdtype == MOE_WEIGHTS_FP8_E4M3;
   if (sh_gate) {
     GemmOperand& v = a.op[1];
     v.w = sh_gate;
@@ -156,8 +157,7 @@ int run_gate_up(const void* x, int T, int H, int E, int k, int I, const void* ga
   a.P = T * k;
   a.E = E;
   a.T = T;
-  hipError_t err = launch_stream_gemm(kModeSwiglu, kRoleGateUp, wdtype == MOE_WEIGHTS_FP8_E4M3, a,
-                                      MT, s);
+  hipError_t err = launch_stream_gemm(kModeSwiglu, kRoleGateUp, a, MT, s);
   if (err == hipErrorInvalidValue)
     return fail(MOE_EINVAL, "gate_up: no kernel configuration for H=%d I=%d IS=%d", H, I, IS);
   return hip_check(err, "gate_up launch");
@@ -168,6 +168,7 @@ int run_down(const void* act, int T, int H, int E, int k, int I, const void* dow
              const int* order, const int* table, int MT, void* y, void* y_sh, hipStream_t s) {
   GemmArgs a{};
   a.op[0] = down_operand(down, dn_scale, H, I, act, y);
+  a.op[0].fp8 = wdtype == MOE_WEIGHTS_FP8_E4M3;
   if (sh_down) {
     GemmOperand& v = a.op[1];
     v.w = sh_down;
@@ -189,8 +190,7 @@ int run_down(const void* act, int T, int H, int E, int k, int I, const void* dow
   a.P = T * k;
   a.E = E;
   a.T = T;
-  hipError_t err = launch_stream_gemm(kModePlain, kRoleDown, wdtype == MOE_WEIGHTS_FP8_E4M3, a,
-                                      MT, s);
+  hipError_t err = launch_stream_gemm(kModePlain, kRoleDown, a, MT, s);
   if (err == hipErrorInvalidValue)
     return fail(MOE_EINVAL, "down: no kernel configuration for H=%d I=%d IS=%d", H, I, IS);
   return hip_check(err, "down launch");
@@ -236,7 +236,7 @@ int moe_router_logits(const void* x, int T, int H, const void* w_pack, int n_pac
   a.E = 0;
   a.T = T;
   int mt = (T + kBM - 1) / kBM;
-  hipError_t err = launch_stream_gemm(kModePlain, kRoleRouter, false, a, mt, (hipStream_t)stream);
+  hipError_t err = launch_stream_gemm(kModePlain, kRoleRouter, a, mt, (hipStream_t)stream);
   if (err == hipErrorInvalidValue) return fail(MOE_EINVAL, "router: no configuration for H=%d", H);
   return hip_check(err, "router launch");
 }
@@ -271,26 +271,35 @@ int moe_sort(const long long* idx64, int T, int k, int E, int bm, int has_shared
 
 int moe_grouped_gate_up(const void* x, int T, int H, int E, int k, int I, const void* gate_up,
                         const float* gu_scale, int wdtype, const int* order, const int* table,
-                        int max_tiles, void* act, void* stream) {
+                        int max_tiles, void* act, const void* sh_gate, const void* sh_up, int IS,
+                        void* act_sh, void* stream) {
   int rc = check_experts_shape(T, H, E, k, I);
   if (rc) return rc;
   CHECK_ARG(wdtype == MOE_WEIGHTS_BF16 || (wdtype == MOE_WEIGHTS_FP8_E4M3 && gu_scale),
             "bad weight dtype / missing scales");
+  CHECK_ARG(x && gate_up && order && table && act, "null pointer");
+  CHECK_ARG(!sh_gate || (sh_up && act_sh && IS >= 32 && IS % 32 == 0 &&
+                         (((intptr_t)sh_up - (intptr_t)sh_gate) & 1) == 0),
+            "shared expert needs sh_up, act_sh and IS a multiple of 32");
   if (T == 0) return MOE_OK;
-  return run_gate_up(x, T, H, E, k, I, gate_up, gu_scale, wdtype, nullptr, nullptr, 0, order,
-                     table, max_tiles, act, nullptr, (hipStream_t)stream);
+  return run_gate_up(x, T, H, E, k, I, gate_up, gu_scale, wdtype, sh_gate, sh_up, IS, order,
+                     table, max_tiles, act, act_sh, (hipStream_t)stream);
 }
 
 int moe_grouped_down(const void* act, int T, int H, int E, int k, int I, const void* down,
                      const float* dn_scale, int wdtype, const int* order, const int* table,
-                     int max_tiles, void* y, void* stream) {
+                     int max_tiles, void* y, const void* sh_down, int IS, const void* act_sh,
+                     void* y_sh, void* stream) {
   int rc = check_experts_shape(T, H, E, k, I);
   if (rc) return rc;
   CHECK_ARG(wdtype == MOE_WEIGHTS_BF16 || (wdtype == MOE_WEIGHTS_FP8_E4M3 && dn_scale),
             "bad weight dtype / missing scales");
+  CHECK_ARG(act && down && order && table && y, "null pointer");
+  CHECK_ARG(!sh_down || (act_sh && y_sh && IS >= 32 && IS % 32 == 0),
+            "shared expert needs act_sh, y_sh and IS a multiple of 32");
   if (T == 0) return MOE_OK;
-  return run_down(act, T, H, E, k, I, down, dn_scale, wdtype, nullptr, 0, nullptr, order, table,
-                  max_tiles, y, nullptr, (hipStream_t)stream);
+  return run_down(act, T, H, E, k, I, down, dn_scale, wdtype, sh_down, IS, act_sh, order, table,
+                  max_tiles, y, y_sh, (hipStream_t)stream);
 }
 
 int moe_combine(const void* y, const void* w, int T, int H, int k, const void* ysh,

@@ -29,6 +29,7 @@ struct GemmOperand {
   long long ld_out;
   int in_map;           // routed: 1 -> B row = token of pair order[r]; 0 -> B row = r
   int out_map;          // routed: 1 -> out row = pair order[r]; 0 -> out row = r
+  int fp8;              // weights are OCP e4m3fn bytes (else bf16)
 };
 
 struct GemmArgs {
@@ -40,7 +41,7 @@ struct GemmArgs {
   int nrb;           // weight-row blocks per tile (set by the launcher)
 };
 
-hipError_t launch_stream_gemm(int mode, int role, bool fp8, const GemmArgs& a, int max_tiles,
+hipError_t launch_stream_gemm(int mode, int role, const GemmArgs& a, int max_tiles,
                               hipStream_t st);
 
 }  // namespace moe

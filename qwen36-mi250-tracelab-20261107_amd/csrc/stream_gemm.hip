@@ -28,11 +28,13 @@
 
 namespace moe {
 
-template <int MODE, int WR, int WK, int S, int TOKB, bool FP8>
+// HAS_FP8: the launch may hold an fp8 operand; each operand's own ``fp8`` flag picks the
+// bf16 or the fp8 main loop (a block's routed experts may be fp8 while its shared expert
+// is bf16).
+template <int MODE, int WR, int WK, int S, int TOKB, bool HAS_FP8>
 __global__ __launch_bounds__(64 * WR * WK) void k_stream_gemm(GemmArgs args) {
   constexpr int kRowsPerWave = 16;
   constexpr int kOutRowsPerWG = (MODE == kModeSwiglu ? 8 : 16) * WR;
-  constexpr int kChunk = FP8 ? 64 * S : 32 * S;  // K elements per lane-group iteration
   constexpr int BM = 16 * TOKB;
   __shared__ f32x4_t red[(WK > 1 ? (WK - 1) : 1) * WR * TOKB * kWave];
 
@@ -98,7 +100,8 @@ __global__ __launch_bounds__(64 * WR * WK) void k_stream_gemm(GemmArgs args) {
   for (int tb = 0; tb < TOKB; ++tb) acc[tb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
   const uint16_t* __restrict__ xin = op.in;
-  if (!FP8) {
+  if (!HAS_FP8 || !op.fp8) {
+    constexpr int kChunk = 32 * S;  // K elements per iteration
     const uint16_t* __restrict__ wp = reinterpret_cast<const uint16_t*>(op.w) + wrow_off + kq * 8;
     for (int kc = 0; kc < Kw; kc += kChunk) {
       uint4 a[S];
@@ -117,6 +120,7 @@ __global__ __launch_bounds__(64 * WR * WK) void k_stream_gemm(GemmArgs args) {
       }
     }
   } else {
+    constexpr int kChunk = 64 * S;
     const uint8_t* __restrict__ wp = reinterpret_cast<const uint8_t*>(op.w) + wrow_off + kq * 16;
     for (int kc = 0; kc < Kw; kc += kChunk) {
       uint4 q[S];
@@ -213,11 +217,11 @@ struct StreamCfg {
   int wr, wk, s;
 };
 
-template <int MODE, bool FP8>
+template <int MODE, bool HAS_FP8>
 static hipError_t launch_cfg(const StreamCfg& c, const GemmArgs& a, int grid, hipStream_t st) {
 #define MOE_L(WR, WK, S)                                                                       \
   if (c.wr == WR && c.wk == WK && c.s == S) {                                                  \
-    hipLaunchKernelGGL((k_stream_gemm<MODE, WR, WK, S, 4, FP8>), dim3(grid), dim3(64 * WR * WK), 0, \
+    hipLaunchKernelGGL((k_stream_gemm<MODE, WR, WK, S, 4, HAS_FP8>), dim3(grid), dim3(64 * WR * WK), 0, \
                        st, a);                                                                 \
     return hipGetLastError();                                                                  \
   }
@@ -234,16 +238,17 @@ static hipError_t launch_cfg(const StreamCfg& c, const GemmArgs& a, int grid, hi
   return hipErrorInvalidConfiguration;
 }
 
-static bool cfg_fits(const StreamCfg& c, int mode, bool fp8, const GemmOperand& op) {
+static bool cfg_fits(const StreamCfg& c, int mode, const GemmOperand& op) {
   if (op.N <= 0) return true;
   int rows = (mode == kModeSwiglu ? 8 : 16) * c.wr;
-  int chunk = (fp8 ? 64 : 32) * c.s;
+  int chunk = (op.fp8 ? 64 : 32) * c.s;
   return op.N % rows == 0 && op.K % (c.wk * chunk) == 0;
 }
 
-hipError_t launch_stream_gemm(int mode, int role, bool fp8, const GemmArgs& a_in, int max_tiles,
+hipError_t launch_stream_gemm(int mode, int role, const GemmArgs& a_in, int max_tiles,
                               hipStream_t st) {
   GemmArgs a = a_in;
+  const bool fp8 = (a.op[0].N > 0 && a.op[0].fp8) || (a.op[1].N > 0 && a.op[1].fp8);
   // Preference lists per role; the first configuration both operands fit is used.
   static const StreamCfg kRouter[] = {{1, 8, 8}, {1, 4, 4}, {1, 1, 1}};
   static const StreamCfg kGateUp[] = {{1, 4, 16}, {1, 4, 8}, {1, 4, 4}, {1, 1, 1}};
@@ -264,7 +269,7 @@ hipError_t launch_stream_gemm(int mode, int role, bool fp8, const GemmArgs& a_in
   for (int i = 0; i < n; ++i) {
     const StreamCfg& c = list[i];
     if (fp8 && c.s == 16) continue;
-    if (cfg_fits(c, mode, fp8, a.op[0]) && cfg_fits(c, mode, fp8, a.op[1])) {
+    if (cfg_fits(c, mode, a.op[0]) && cfg_fits(c, mode, a.op[1])) {
       pick = &list[i];
       break;
     }

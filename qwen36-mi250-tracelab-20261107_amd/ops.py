@@ -155,8 +155,10 @@ def sort_pairs(top_k_index: torch.Tensor, experts: int, bm: int | None = None,
 
 
 def grouped_gate_up(x: torch.Tensor, top_k: int, gate_up: torch.Tensor, sp: SortedPairs,
-                    scale: torch.Tensor | None = None) -> torch.Tensor:
-    """act [T*k, I] in sorted-row order: bf16(bf16(silu(bf16 g)) * bf16 u)."""
+                    scale: torch.Tensor | None = None, shared=None):
+    """act [T*k, I] in sorted-row order: bf16(bf16(silu(bf16 g)) * bf16 u).
+    ``shared`` = (gate_proj.weight, up_proj.weight) of the shared expert (the table must
+    be built with ``shared=True``): returns (act, act_shared [T, IS]) from one launch."""
     _need_cuda(x, gate_up)
     x = _bf16(x, "x")
     w, s, wd = expert_weight(gate_up, scale, "gate_up")
@@ -167,27 +169,40 @@ def grouped_gate_up(x: torch.Tensor, top_k: int, gate_up: torch.Tensor, sp: Sort
     experts, two_i, _ = w.shape
     inter = two_i // 2
     act = torch.empty((tokens * top_k, inter), dtype=torch.bfloat16, device=x.device)
+    sg = su = act_sh = None
+    inter_s = 0
+    if shared is not None:
+        sg, su = (_bf16(t, "shared weight") for t in shared)
+        inter_s = sg.shape[0]
+        act_sh = torch.empty((tokens, inter_s), dtype=torch.bfloat16, device=x.device)
     lib = _lib.load()
     check(lib.moe_grouped_gate_up(ptr(x), tokens, hidden, experts, top_k, inter, ptr(w), ptr(s), wd,
-                                  ptr(sp.order), ptr(sp.table), sp.max_tiles, ptr(act),
-                                  stream_of(x)), "grouped_gate_up")
-    return act
+                                  ptr(sp.order), ptr(sp.table), sp.max_tiles, ptr(act), ptr(sg),
+                                  ptr(su), inter_s, ptr(act_sh), stream_of(x)), "grouped_gate_up")
+    return act if shared is None else (act, act_sh)
 
 
 def grouped_down(act: torch.Tensor, tokens: int, top_k: int, down: torch.Tensor, sp: SortedPairs,
-                 scale: torch.Tensor | None = None) -> torch.Tensor:
-    """y [T*k, H]: bf16(act[r] . Wd[e]) written at pair order[r]'s own row."""
+                 scale: torch.Tensor | None = None, shared=None):
+    """y [T*k, H]: bf16(act[r] . Wd[e]) written at pair order[r]'s own row.
+    ``shared`` = (down_proj.weight, act_shared): returns (y, y_shared [T, H])."""
     _need_cuda(act, down)
     act = _bf16(act, "act")
     w, s, wd = expert_weight(down, scale, "down")
     _check_row_major(w)
     experts, hidden, inter = w.shape
     y = torch.empty((tokens * top_k, hidden), dtype=torch.bfloat16, device=act.device)
+    sd = act_sh = y_sh = None
+    inter_s = 0
+    if shared is not None:
+        sd, act_sh = _bf16(shared[0], "shared down"), _bf16(shared[1], "act_shared")
+        inter_s = sd.shape[1]
+        y_sh = torch.empty((tokens, hidden), dtype=torch.bfloat16, device=act.device)
     lib = _lib.load()
     check(lib.moe_grouped_down(ptr(act), tokens, hidden, experts, top_k, inter, ptr(w), ptr(s), wd,
-                               ptr(sp.order), ptr(sp.table), sp.max_tiles, ptr(y), stream_of(act)),
-          "grouped_down")
-    return y
+                               ptr(sp.order), ptr(sp.table), sp.max_tiles, ptr(y), ptr(sd),
+                               inter_s, ptr(act_sh), ptr(y_sh), stream_of(act)), "grouped_down")
+    return y if shared is None else (y, y_sh)
 
 
 def combine(y: torch.Tensor, top_w: torch.Tensor, shared: torch.Tensor | None = None,

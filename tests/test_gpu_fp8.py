@@ -1,0 +1,102 @@
+"""fp8-e4m3 expert weights on the GPU (C5's format; the reference has no fp8 path, so
+these pin the format and the arithmetic independently).
+
+Tolerances (stated separately from bf16, as the north star asks):
+- against the fp32 oracle on the dequantised weights (scale * q): the bf16 bar,
+  max-abs <= 2e-2 and mean-rel <= 5e-3 (plus the reference path's own bf16 error);
+- against the fp32 oracle on the bf16 masters: mean-rel <= 6e-2 and max-abs <= 5e-2,
+  the per-row e4m3 quantisation error (3 mantissa bits, ~2^-5 relative per weight,
+  averaged down over K) measured on these synthetic layers.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle import moe_oracle as orc
+from tests.helpers import BF16, max_abs, mean_rel
+
+pytestmark = pytest.mark.gpu
+
+
+def test_fp8_dequant_every_encoding(pkg, dev):
+    """y = act . W^T with one-hot act rows reads back every e4m3fn byte exactly."""
+    E, H, I, T = 1, 256, 256, 256
+    n = torch.arange(H)[:, None]
+    k = torch.arange(I)[None, :]
+    b = ((n + k) % 256).to(torch.uint8)
+    b[(b == 0x7F) | (b == 0xFF)] = 0  # the two NaN encodings
+    q = b.view(torch.float8_e4m3fn).reshape(E, H, I).to(dev)
+    scale = torch.ones(E, H, dtype=torch.float32, device=dev)
+    idx = torch.zeros(T, 1, dtype=torch.long, device=dev)
+    sp = pkg.ops.sort_pairs(idx, E)
+    act = torch.eye(T, I, dtype=BF16, device=dev)
+    y = pkg.ops.grouped_down(act, T, 1, q, sp, scale=scale)
+    torch.cuda.synchronize()
+    want = q[0].float().T.cpu()  # y[p, n] = W[n, p]
+    assert torch.equal(y.float().cpu(), want)
+
+
+def _fp8_weights(w):
+    q, s = orc.quantize_rows(w["gate_up"])
+    q2, s2 = orc.quantize_rows(w["down"])
+    return q, s, q2, s2
+
+
+@pytest.mark.parametrize("n", [1, 8, 40])
+def test_fp8_experts_match_dequantised_oracle(pkg, dev, n):
+    H, E, K, I = 256, 16, 4, 128
+    w = orc.make_weights(H, E, I, I, seed=3)
+    q, s, q2, s2 = _fp8_weights(w)
+    g = torch.Generator().manual_seed(n)
+    x = torch.randn(n, H, generator=g).to(BF16)
+    logits = torch.nn.functional.linear(x, w["router"])
+    tw, ti = orc.route(logits, K)
+    out = pkg.ops.experts(x.to(dev), ti.to(dev), tw.to(dev), q.to(dev), q2.to(dev),
+                          round_products=n <= 16, gate_up_scale=s.to(dev), down_scale=s2.to(dev))
+    torch.cuda.synchronize()
+    deq = {"gate_up": orc.dequantize_rows(q, s), "down": orc.dequantize_rows(q2, s2)}
+    ref = torch.zeros(n, H)
+    for t in range(n):
+        for j in range(K):
+            e = int(ti[t, j])
+            gu = deq["gate_up"][e] @ x[t].float()
+            a = torch.nn.functional.silu(gu[:I]) * gu[I:]
+            ref[t] += tw[t, j].float() * (deq["down"][e] @ a)
+    assert max_abs(out, ref) <= 2e-2 and mean_rel(out, ref) <= 1e-2
+
+
+@pytest.mark.parametrize("T", [1, 32])
+def test_fp8_block_full_shape(pkg, dev, T):
+    """C5's layer shape: fp8 routed experts, bf16 router / shared expert."""
+    import __graft_entry__
+
+    Hh, E, I = 2048, 256, 512
+    gen = torch.Generator(device=dev).manual_seed(11)
+
+    def rnd(*shape):
+        return (torch.randn(*shape, generator=gen, device=dev) * 0.02).to(BF16)
+
+    w = {"router": rnd(E, Hh), "gate_up": rnd(E, 2 * I, Hh), "down": rnd(E, Hh, I),
+         "sh_gate": rnd(I, Hh), "sh_up": rnd(I, Hh), "sh_down": rnd(Hh, I), "sh_gate_w": rnd(1, Hh)}
+    mlp = __graft_entry__._mlp_from_weights(w, dev)
+    q, s = pkg.fp8.quantize_rows(w["gate_up"])
+    q2, s2 = pkg.fp8.quantize_rows(w["down"])
+    mlp.experts.gate_up_proj, mlp.experts.gate_up_scale = q, s
+    mlp.experts.down_proj, mlp.experts.down_scale = q2, s2
+    x = torch.randn(T, Hh, generator=torch.Generator().manual_seed(T)).to(BF16)
+    out, idx, wts, logits = pkg.block.moe(x.to(dev), mlp, 8, return_routing=True)
+    torch.cuda.synchronize()
+    lg = logits.cpu()[:, :E]
+    _, ref_i = orc.route(lg, 8)
+    assert torch.equal(idx.cpu(), ref_i)
+    wq = dict(w, gate_up=q, down=q2, gate_up_scale=s, down_scale=s2)
+    f32_q = orc.block_fp32(x, wq, ref_i, logits=lg)
+    f32_m = orc.block_fp32(x, w, ref_i, logits=lg)
+    print(f"fp8 T={T}: vs dequantised fp32 max {max_abs(out, f32_q):.3g} mean-rel "
+          f"{mean_rel(out, f32_q):.3g}; vs bf16 masters max {max_abs(out, f32_m):.3g} mean-rel "
+          f"{mean_rel(out, f32_m):.3g}", flush=True)
+    assert torch.isfinite(out.float()).all()
+    assert max_abs(out, f32_q) <= 2e-2 and mean_rel(out, f32_q) <= 6e-3
+    assert max_abs(out, f32_m) <= 5e-2 and mean_rel(out, f32_m) <= 6e-2
