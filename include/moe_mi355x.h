@@ -46,8 +46,10 @@ extern "C" {
 int moe_abi_version(void);
 const char* moe_last_error(void);
 
-/* Rows of the tile table's token tiles used by the fused entry points. */
-int moe_tile_rows(void);
+/* Sorted rows per tile (bm) the fused entry points use for T tokens: 16 up to 16 tokens,
+ * 32 up to 512, 64 above. A table passed to moe_grouped_gate_up / moe_grouped_down must be
+ * built with a bm of 16, 32, 64 or 128. */
+int moe_tile_rows(int T);
 
 /* Tile-table capacity for T tokens: ceil(T*k/bm) + min(E, T*k) (+ ceil(T/bm) shared tiles). */
 int moe_max_tiles(int T, int k, int E, int bm, int has_shared);
@@ -56,7 +58,8 @@ int moe_max_tiles(int T, int k, int E, int bm, int has_shared);
  * modeling_qwen3_5_moe.py:768-769 / engine/fast/model.py:1159 and the packed
  * router|shared-gate GEMV of engine/fast/fused.py:745-746 + mfma.py:90-119.
  * w_pack [n_pack, H] bf16: rows 0..E-1 the router, row E the shared-expert gate
- * (shared_expert_gate.weight), the rest zero; n_pack a multiple of 16.
+ * (shared_expert_gate.weight), the rest zero; n_pack a multiple of 16 (64 lets the
+ * 64-row weight blocks of prefill-sized batches apply).
  * logits [T, n_pack] = bf16(x . w_pack^T). */
 int moe_router_logits(const void* x, int T, int H, const void* w_pack, int n_pack, void* logits,
                       void* stream);
@@ -88,8 +91,8 @@ int moe_sort(const long long* idx64, int T, int k, int E, int bm, int has_shared
  * computes the shared expert's act_sh [T, IS] (a6; prefill_kernels.py:232-251). */
 int moe_grouped_gate_up(const void* x, int T, int H, int E, int k, int I, const void* gate_up,
                         const float* gu_scale, int wdtype, const int* order, const int* table,
-                        int max_tiles, void* act, const void* sh_gate, const void* sh_up, int IS,
-                        void* act_sh, void* stream);
+                        int max_tiles, int bm, void* act, const void* sh_gate, const void* sh_up,
+                        int IS, void* act_sh, void* stream);
 
 /* Grouped expert down (a5 / a9): y[order[r]] = bf16(act[r] . Wd[e]) at each pair's own row.
  * Replaces moe_prefill._down_kernel / _down_stream_kernel (moe_prefill.py:212-319).
@@ -97,8 +100,8 @@ int moe_grouped_gate_up(const void* x, int T, int H, int E, int k, int I, const 
  * With sh_down [H, IS] the same launch also writes y_sh [T, H] = bf16(act_sh . Wsd). */
 int moe_grouped_down(const void* act, int T, int H, int E, int k, int I, const void* down,
                      const float* dn_scale, int wdtype, const int* order, const int* table,
-                     int max_tiles, void* y, const void* sh_down, int IS, const void* act_sh,
-                     void* y_sh, void* stream);
+                     int max_tiles, int bm, void* y, const void* sh_down, int IS,
+                     const void* act_sh, void* y_sh, void* stream);
 
 /* Combine (a7 / a10): out[t] = bf16(bf16(sum_j term(y[t*k+j], w[t,j]))
  *   + bf16(bf16(sigmoid(seg[t])) * ysh[t])) (+ residual). Replaces

@@ -32,16 +32,16 @@ _SZ = ctypes.c_size_t
 SIGNATURES: dict[str, tuple] = {
     "moe_abi_version": (_I, []),
     "moe_last_error": (ctypes.c_char_p, []),
-    "moe_tile_rows": (_I, []),
+    "moe_tile_rows": (_I, [_I]),
     "moe_max_tiles": (_I, [_I, _I, _I, _I, _I]),
     "moe_router_logits": (_I, [_P, _I, _I, _P, _I, _P, _P]),
     "moe_route_topk": (_I, [_P, _LL, _I, _I, _I, _P, _P, _P, _P]),
     "moe_sort_scratch_bytes": (_SZ, [_I, _I]),
     "moe_sort": (_I, [_P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _I, _P, _P]),
     "moe_grouped_gate_up": (
-        _I, [_P, _I, _I, _I, _I, _I, _P, _P, _I, _P, _P, _I, _P, _P, _P, _I, _P, _P]),
+        _I, [_P, _I, _I, _I, _I, _I, _P, _P, _I, _P, _P, _I, _I, _P, _P, _P, _I, _P, _P]),
     "moe_grouped_down": (
-        _I, [_P, _I, _I, _I, _I, _I, _P, _P, _I, _P, _P, _I, _P, _P, _I, _P, _P, _P]),
+        _I, [_P, _I, _I, _I, _I, _I, _P, _P, _I, _P, _P, _I, _I, _P, _P, _I, _P, _P, _P]),
     "moe_combine": (_I, [_P, _P, _I, _I, _I, _P, _P, _LL, _P, _P, _I, _P]),
     "moe_experts_workspace_bytes": (_SZ, [_I, _I, _I, _I, _I]),
     "moe_experts_forward": (

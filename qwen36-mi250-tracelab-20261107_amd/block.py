@@ -35,7 +35,7 @@ _PACK_ATTR = "_mi355x_router_pack"
 
 def pack_router(mlp) -> torch.Tensor:
     """The router rows and the shared-expert gate row as one [n_pack, H] bf16 tensor
-    (rows 0..E-1 router, row E shared gate, zero rows up to a multiple of 16), built once
+    (rows 0..E-1 router, row E shared gate, zero rows up to a multiple of 64), built once
     per block and cached on it (the packing engine/fast/fused.py:699-746 does for its
     router|shared GEMV). Rebuilt when either source weight changes."""
     router = mlp.gate.weight
@@ -45,7 +45,7 @@ def pack_router(mlp) -> torch.Tensor:
     if cached is not None and cached[0] == key:
         return cached[1]
     experts, hidden = router.shape
-    n_pack = (experts + 1 + 15) // 16 * 16
+    n_pack = (experts + 1 + 63) // 64 * 64
     pack = torch.zeros((n_pack, hidden), dtype=torch.bfloat16, device=router.device)
     with torch.no_grad():
         pack[:experts].copy_(router)

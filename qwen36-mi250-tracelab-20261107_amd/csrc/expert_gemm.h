@@ -1,4 +1,4 @@
-// Arguments of the expert-grouped weight-streaming GEMM (stream_gemm.hip).
+// Arguments of the expert-grouped MFMA GEMM (expert_gemm.hip).
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -41,7 +41,9 @@ struct GemmArgs {
   int nrb;           // weight-row blocks per tile (set by the launcher)
 };
 
-hipError_t launch_stream_gemm(int mode, int role, const GemmArgs& a, int max_tiles,
+// Launches k_expert_gemm over max_tiles tiles of at most bm (16, 32 or 64) sorted rows.
+// hipErrorInvalidValue: no kernel configuration fits the operands' shapes.
+hipError_t launch_expert_gemm(int mode, int role, int bm, const GemmArgs& a, int max_tiles,
                               hipStream_t st);
 
 }  // namespace moe

@@ -1,0 +1,416 @@
+// Expert-grouped MFMA GEMM for gfx950 with weights streamed from HBM and token rows staged
+// through LDS (subsystems a1, a4, a5, a6, a8, a9, a12).
+//
+// One kernel serves every projection of the MoE block:
+//   * router logits        out[t, n]  = bf16(x_t . Wr[n])                 (PLAIN)
+//   * expert gate_up       act[r, n]  = bf16(bf16(silu(bf16 g)) * bf16 u)  (SWIGLU)
+//                          g = x_tok(r) . Wg[e, n], u = x_tok(r) . Wu[e, n]
+//   * expert down          y[pair(r), n] = bf16(act[r] . Wd[e, n])          (PLAIN)
+// The rounding points are those of Transformers' batched_mm experts path
+// (transformers/integrations/moe.py:112-176), of engine/fast/kernels.py:88-164 and of the
+// grouped kernels engine/fast/moe_prefill.py:156-257.
+//
+// Work decomposition. The sort kernel groups the (token, expert) pairs by expert into
+// tiles of up to BM = 16 * TOKB sorted rows of ONE expert (the tile table). A workgroup
+// takes one tile and one block of weight rows; every weight element of the block is read
+// from HBM once per tile and multiplied against all of the tile's tokens (expert
+// de-duplication across the batch).
+//
+// A workgroup has WR x WK waves. Wave (wr, wk) owns 16 weight rows (SWIGLU: 8 gate rows and
+// the matching 8 up rows, paired in registers by the epilogue) and the wk-th of WK slices
+// of K; the K partial sums are reduced through LDS in a fixed order (deterministic).
+// * A operand (weights): straight from HBM into registers in the v_mfma_f32_16x16x32_bf16
+//   A layout (lane = row l%16, 8 consecutive k at 8*(l/16)); 64 contiguous bytes of each of
+//   16 rows per load instruction; a ring of NA chunks of KC k-values is kept in flight.
+// * B operand (token rows): the WR waves of a K slice stage each chunk of the tile's token
+//   rows in LDS with row-contiguous 256-byte loads (four rows per instruction), double
+//   buffered, and read it back in the MFMA B layout (conflict-free: 272-byte row pitch).
+// fp8-e4m3 weights (per-output-row fp32 scales) are converted to bf16 in registers (exact)
+// and the scale multiplies the fp32 accumulator before the bf16 rounding:
+// sum_k s_n q_nk x_k = s_n sum_k q_nk x_k.
+#include "moe_common.h"
+#include "expert_gemm.h"
+
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+namespace moe {
+
+// KC: K elements per chunk (128; 32 for small test shapes, bf16 only); R: chunks in flight.
+template <int MODE, int WR, int WK, int TOKB, bool HAS_FP8, int KC, int R = 4>
+__global__ __launch_bounds__(64 * WR * WK) void k_expert_gemm(GemmArgs args) {
+  constexpr int kRowU4 = KC / 8;        // uint4 per staged token-row chunk (bf16)
+  constexpr int kPitchU4 = kRowU4 + 1;  // LDS row pitch in uint4 (conflict-free B reads)
+  constexpr int LPC16 = KC / 32;        // bf16 weight loads per lane per chunk
+  constexpr int LPC8 = KC / 64;         // fp8 weight loads per lane per chunk
+  constexpr int LPCA = LPC16;           // ring entries per chunk (fp8 uses LPC8 of them)
+  static_assert(!HAS_FP8 || LPC8 >= 1, "fp8 needs KC >= 64");
+  constexpr int kOutRowsPerWG = (MODE == kModeSwiglu ? 8 : 16) * WR;
+  constexpr int BM = 16 * TOKB;
+  constexpr int LPR = kRowU4;                  // staging lanes per token row
+  constexpr int RPI = 64 / LPR;                // token rows per staging instruction
+  constexpr int STG = (TOKB * 16) / (RPI * WR);  // staging instructions per wave per chunk
+  static_assert(STG >= 1 && STG * RPI * WR == TOKB * 16, "staging split");
+  constexpr int kBufU4 = TOKB * 16 * kPitchU4;  // one chunk of one K slice
+  // LDS: [WK][2 buffers][TOKB*16 rows][pitch] uint4; reused for the K-split reduction.
+  __shared__ uint4 lds[WK * 2 * kBufU4];
+
+  const int nrb = args.nrb;
+  const int tile = blockIdx.x / nrb;
+  const int rb = blockIdx.x - tile * nrb;
+
+  int e, r0, r1;
+  if (args.table) {
+    if (tile >= args.table[3 * args.MT]) return;
+    e = args.table[tile];
+    r0 = args.table[args.MT + tile];
+    r1 = args.table[2 * args.MT + tile];
+  } else {
+    e = args.E;
+    r0 = args.P + tile * BM;
+    if (r0 >= args.P + args.T) return;
+    r1 = min(r0 + BM, args.P + args.T);
+  }
+  const bool routed = e < args.E;
+  const GemmOperand& op = routed ? args.op[0] : args.op[1];
+  if (rb * kOutRowsPerWG >= op.N) return;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int wr = wave % WR;
+  const int wk = wave / WR;
+  const int lr = lane & 15;
+  const int kq = lane >> 4;
+  const int Kw = op.K / WK;
+  const int kbeg = wk * Kw;
+  const int nch = Kw / KC;
+  const int ntb = (r1 - r0 + 15) >> 4;
+  const bool use_fp8 = HAS_FP8 && op.fp8;
+
+  // ---- A operand: this lane's weight row, first NA chunks requested at once.
+  long long wrow_off;
+  int obase;  // first output row (PLAIN) / gate row (SWIGLU) of the wave
+  if (MODE == kModeSwiglu) {
+    obase = rb * kOutRowsPerWG + wr * 8;
+    wrow_off = (long long)(obase + (lr & 7)) * op.ldw + (lr >= 8 ? op.up_off : 0);
+  } else {
+    obase = rb * kOutRowsPerWG + wr * 16;
+    wrow_off = (long long)(obase + lr) * op.ldw;
+  }
+  wrow_off += (long long)(routed ? e : 0) * op.estride + kbeg;
+  const uint16_t* __restrict__ wp16 = reinterpret_cast<const uint16_t*>(op.w) + wrow_off + kq * 8;
+  const uint8_t* __restrict__ wp8 = reinterpret_cast<const uint8_t*>(op.w) + wrow_off + kq * 16;
+
+  // ---- B staging: this lane moves 16 bytes of STG token rows per chunk into LDS.
+  // Staging row q = (i * WR + wr) * RPI + lane / LPR, part = lane % LPR (i < STG).
+  const int part = lane % LPR;
+  const int qlane = lane / LPR;
+  long long srow[STG];
+#pragma unroll
+  for (int i = 0; i < STG; ++i) {
+    int q = (i * WR + wr) * RPI + qlane;
+    srow[i] = min(r0 + q, r1 - 1);
+  }
+
+  // The weights of the first chunk are requested before the token-row lookups: they depend
+  // only on the tile, so their HBM latency overlaps the lookups.
+  uint4 aring[R][LPCA];
+  if (!use_fp8) {
+#pragma unroll
+    for (int s = 0; s < LPC16; ++s) aring[0][s] = ld16(wp16 + s * 32);
+  } else if (HAS_FP8) {
+#pragma unroll
+    for (int s = 0; s < LPC8; ++s) aring[0][s] = ld16(wp8 + s * 64);
+  }
+
+  if (!routed) {
+#pragma unroll
+    for (int i = 0; i < STG; ++i) srow[i] -= args.P;
+  } else if (op.in_map) {
+#pragma unroll
+    for (int i = 0; i < STG; ++i) srow[i] = args.order[srow[i]];
+#pragma unroll
+    for (int i = 0; i < STG; ++i) srow[i] /= args.topk;
+  }
+  const uint16_t* __restrict__ xin = op.in;
+#pragma unroll
+  for (int i = 0; i < STG; ++i) srow[i] = srow[i] * op.ld_in + kbeg + part * 8;
+  // Rows past the tile's last 16-row block are not needed.
+  bool sneed[STG];
+#pragma unroll
+  for (int i = 0; i < STG; ++i) sneed[i] = ((i * WR + wr) * RPI) < ntb * 16;
+  uint4* bsl = lds + wk * 2 * kBufU4;  // this K slice's two buffers
+  auto stage_slot = [&](int i) { return ((i * WR + wr) * RPI + qlane) * kPitchU4 + part; };
+
+  // Load stream per chunk m (vmcnt retires in order): A(m) then B(m + 1), each issued R
+  // chunks ahead, so waiting for one chunk's data never drains the rest of the ring.
+  uint4 bring[R][STG];
+  {
+    uint4 b0[STG];
+#pragma unroll
+    for (int i = 0; i < STG; ++i)
+      if (sneed[i]) b0[i] = ld16(xin + srow[i]);
+#pragma unroll
+    for (int m = 0; m < R; ++m) {
+      if (m > 0 && m < nch) {
+        if (!use_fp8) {
+#pragma unroll
+          for (int s = 0; s < LPC16; ++s) aring[m][s] = ld16(wp16 + m * KC + s * 32);
+        } else if (HAS_FP8) {
+#pragma unroll
+          for (int s = 0; s < LPC8; ++s) aring[m][s] = ld16(wp8 + m * KC + s * 64);
+        }
+      }
+      if (m + 1 < nch) {
+#pragma unroll
+        for (int i = 0; i < STG; ++i)
+          if (sneed[i]) bring[(m + 1) % R][i] = ld16(xin + srow[i] + (m + 1) * KC);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < STG; ++i)
+      if (sneed[i]) bsl[stage_slot(i)] = b0[i];
+  }
+  __syncthreads();
+
+  f32x4_t acc[TOKB];
+#pragma unroll
+  for (int tb = 0; tb < TOKB; ++tb) acc[tb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  // ---- main loop over chunks; ring slot = chunk % R
+  for (int c0 = 0; c0 < nch; c0 += R) {
+#pragma unroll
+    for (int cc = 0; cc < R; ++cc) {
+      const int c = c0 + cc;
+      if (c >= nch) break;
+      const uint4* bcur = bsl + (c & 1) * kBufU4;
+      uint4 a4[LPC16];
+      if (!use_fp8) {
+#pragma unroll
+        for (int s = 0; s < LPC16; ++s) a4[s] = aring[cc][s];
+      } else if (HAS_FP8) {
+#pragma unroll
+        for (int s = 0; s < LPC8; ++s) fp8x16_to_bf16(aring[cc][s], a4[2 * s], a4[2 * s + 1]);
+      }
+#pragma unroll
+      for (int tb = 0; tb < TOKB; ++tb) {
+        if (tb < ntb) {
+          const uint4* brow = bcur + (tb * 16 + lr) * kPitchU4;
+          uint4 b[LPC16];
+          if (!use_fp8) {
+#pragma unroll
+            for (int s = 0; s < LPC16; ++s) b[s] = brow[s * 4 + kq];
+          } else if (HAS_FP8) {
+            // fp8 A lane kq holds k = s2*64 + kq*16 + h*8 (+0..7)
+#pragma unroll
+            for (int s2 = 0; s2 < LPC8; ++s2)
+#pragma unroll
+              for (int h = 0; h < 2; ++h) b[s2 * 2 + h] = brow[s2 * 8 + kq * 2 + h];
+          }
+#pragma unroll
+          for (int s = 0; s < LPC16; ++s) acc[tb] = mfma16x16x32(a4[s], b[s], acc[tb]);
+        }
+      }
+      // next chunk's token rows into the other LDS buffer
+      if (c + 1 < nch) {
+        uint4* bnext = bsl + ((c + 1) & 1) * kBufU4;
+#pragma unroll
+        for (int i = 0; i < STG; ++i)
+          if (sneed[i]) bnext[stage_slot(i)] = bring[(cc + 1) % R][i];
+      }
+      // refill: A(c + R) into this slot, B(c + 1 + R) into the slot just drained
+      if (c + R < nch) {
+        if (!use_fp8) {
+#pragma unroll
+          for (int s = 0; s < LPC16; ++s) aring[cc][s] = ld16(wp16 + (c + R) * KC + s * 32);
+        } else if (HAS_FP8) {
+#pragma unroll
+          for (int s = 0; s < LPC8; ++s) aring[cc][s] = ld16(wp8 + (c + R) * KC + s * 64);
+        }
+      }
+      if (c + 1 + R < nch) {
+#pragma unroll
+        for (int i = 0; i < STG; ++i)
+          if (sneed[i]) bring[(cc + 1) % R][i] = ld16(xin + srow[i] + (c + 1 + R) * KC);
+      }
+      __syncthreads();
+    }
+  }
+
+  // ---- K-split reduction through LDS (buffers reused), summed in wk order by wk == 0.
+  if (WK > 1) {
+    f32x4_t* red = reinterpret_cast<f32x4_t*>(lds);
+    if (wk > 0) {
+#pragma unroll
+      for (int tb = 0; tb < TOKB; ++tb)
+        if (tb < ntb) red[(((wk - 1) * WR + wr) * TOKB + tb) * kWave + lane] = acc[tb];
+    }
+    __syncthreads();
+    if (wk > 0) return;
+#pragma unroll
+    for (int v = 1; v < WK; ++v)
+#pragma unroll
+      for (int tb = 0; tb < TOKB; ++tb)
+        if (tb < ntb) acc[tb] += red[(((v - 1) * WR + wr) * TOKB + tb) * kWave + lane];
+  }
+
+  // ---- epilogue. Lane (q = lane / 16, j = lane % 16) holds rows 4q..4q+3 of token column j.
+  const int q = kq;
+  const int j = lr;
+  const float* sc = op.scale ? op.scale + (long long)(routed ? e : 0) * op.sstride : nullptr;
+#pragma unroll
+  for (int tb = 0; tb < TOKB; ++tb) {
+    if (tb >= ntb) break;
+    f32x4_t v = acc[tb];
+    int rr = r0 + tb * 16 + j;
+    if (MODE == kModeSwiglu) {
+      f32x4_t up;
+      up[0] = __shfl_down(v[0], 32);
+      up[1] = __shfl_down(v[1], 32);
+      up[2] = __shfl_down(v[2], 32);
+      up[3] = __shfl_down(v[3], 32);
+      if (q >= 2 || rr >= r1) continue;
+      int n = obase + 4 * q;
+      float o[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float g = v[i], u = up[i];
+        if (sc) {
+          g *= sc[n + i];
+          u *= sc[op.s_up_off + n + i];
+        }
+        g = rbf(g);
+        u = rbf(u);
+        float a = rbf(siluf_(g));
+        o[i] = a * u;
+      }
+      long long orow = routed ? (op.out_map ? args.order[rr] : rr) : rr - args.P;
+      uint2 pk = make_uint2(pack_bf2(o[0], o[1]), pack_bf2(o[2], o[3]));
+      *reinterpret_cast<uint2*>(op.out + orow * op.ld_out + n) = pk;
+    } else {
+      if (rr >= r1) continue;
+      int n = obase + 4 * q;
+      float o[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[i] = sc ? v[i] * sc[n + i] : v[i];
+      long long orow = routed ? (op.out_map ? args.order[rr] : rr) : rr - args.P;
+      uint2 pk = make_uint2(pack_bf2(o[0], o[1]), pack_bf2(o[2], o[3]));
+      *reinterpret_cast<uint2*>(op.out + orow * op.ld_out + n) = pk;
+    }
+  }
+}
+
+// ------------------------------------------------------------------------ dispatch
+
+namespace {
+
+struct Cfg {
+  int wr, wk, tokb, kc;
+};
+
+template <int MODE, bool HAS_FP8>
+hipError_t launch_cfg(const Cfg& c, const GemmArgs& a, int grid, hipStream_t st) {
+#define MOE_L(WR, WK, TOKB, KCV)                                                                \
+  if (c.wr == WR && c.wk == WK && c.tokb == TOKB && c.kc == KCV) {                              \
+    hipLaunchKernelGGL((k_expert_gemm<MODE, WR, WK, TOKB, HAS_FP8, KCV>), dim3(grid),           \
+                       dim3(64 * WR * WK), 0, st, a);                                           \
+    return hipGetLastError();                                                                   \
+  }
+  MOE_L(1, 4, 1, 128)
+  MOE_L(1, 2, 1, 128)
+  MOE_L(1, 1, 1, 128)
+  MOE_L(4, 1, 4, 128)
+  MOE_L(4, 1, 1, 128)
+  MOE_L(2, 2, 2, 128)
+  MOE_L(2, 1, 2, 128)
+  MOE_L(1, 4, 1, 64)
+  MOE_L(4, 1, 4, 64)
+  MOE_L(2, 2, 2, 64)
+  MOE_L(2, 1, 2, 64)
+  MOE_L(4, 1, 8, 64)
+  MOE_L(2, 1, 8, 64)
+  if constexpr (!HAS_FP8) {
+    MOE_L(1, 1, 1, 32)
+    MOE_L(1, 1, 2, 32)
+    MOE_L(1, 1, 4, 32)
+  }
+#undef MOE_L
+  return hipErrorInvalidConfiguration;
+}
+
+bool fits(const Cfg& c, int mode, const GemmOperand& op) {
+  if (op.N <= 0) return true;
+  int rows = (mode == kModeSwiglu ? 8 : 16) * c.wr;
+  if (op.fp8 && c.kc < 64) return false;
+  return op.N % rows == 0 && op.K % (c.wk * c.kc) == 0;
+}
+
+// MOE_GEMM_CFG="router=wr,wk;gate_up=wr,wk;down=wr,wk" overrides the choice for a role
+// (tuning knob; read at each launch). TOKB follows from the tile rows.
+bool env_cfg(int role, Cfg* out) {
+  const char* env = getenv("MOE_GEMM_CFG");
+  if (!env) return false;
+  const char* names[] = {"router=", "gate_up=", "down="};
+  const char* p = strstr(env, names[role]);
+  if (!p) return false;
+  Cfg c{};
+  c.kc = 128;
+  if (sscanf(p + strlen(names[role]), "%d,%d,%d", &c.wr, &c.wk, &c.kc) < 2) return false;
+  *out = c;
+  return true;
+}
+
+}  // namespace
+
+hipError_t launch_expert_gemm(int mode, int role, int bm, const GemmArgs& a_in, int max_tiles,
+                              hipStream_t st) {
+  GemmArgs a = a_in;
+  const bool fp8 = (a.op[0].N > 0 && a.op[0].fp8) || (a.op[1].N > 0 && a.op[1].fp8);
+  const int tokb = bm / 16;
+  if (bm % 16 || (tokb != 1 && tokb != 2 && tokb != 4 && tokb != 8)) return hipErrorInvalidValue;
+  // Preferences: with one 16-token block per tile, split K over 4 waves (more waves for the
+  // few-token decode case); with 4 blocks, 4 row groups share the staged token rows.
+  Cfg prefs[6];
+  int n = 0;
+  Cfg forced;
+  if (env_cfg(role, &forced)) {
+    forced.tokb = tokb;
+    prefs[n++] = forced;
+  }
+  (void)0;
+  if (tokb == 1) {
+    prefs[n++] = {1, 4, 1, 64};
+    prefs[n++] = {1, 2, 1, 128};
+    prefs[n++] = {1, 1, 1, 128};
+  } else if (tokb == 2) {
+    prefs[n++] = role == kRoleDown ? Cfg{2, 1, 2, 64} : Cfg{2, 2, 2, 64};
+    prefs[n++] = {2, 1, 2, 64};
+  } else if (tokb == 4) {
+    prefs[n++] = {4, 1, 4, 64};
+  } else {
+    prefs[n++] = {4, 1, 8, 64};
+  }
+  prefs[n++] = {1, 1, tokb, 32};  // small test shapes (K a multiple of 32)
+  const Cfg* pick = nullptr;
+  for (int i = 0; i < n; ++i)
+    if (fits(prefs[i], mode, a.op[0]) && fits(prefs[i], mode, a.op[1]) &&
+        prefs[i].wk * 2 * prefs[i].tokb * 16 * (prefs[i].kc / 8 + 1) * 16 <= 65536) {
+      pick = &prefs[i];
+      break;
+    }
+  if (!pick) return hipErrorInvalidValue;
+  int rows = (mode == kModeSwiglu ? 8 : 16) * pick->wr;
+  int nmax = a.op[0].N > a.op[1].N ? a.op[0].N : a.op[1].N;
+  a.nrb = nmax / rows;
+  if (a.nrb <= 0 || max_tiles <= 0) return hipSuccess;
+  long long grid = (long long)max_tiles * a.nrb;
+  if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
+  if (mode == kModeSwiglu)
+    return fp8 ? launch_cfg<kModeSwiglu, true>(*pick, a, (int)grid, st)
+               : launch_cfg<kModeSwiglu, false>(*pick, a, (int)grid, st);
+  return fp8 ? launch_cfg<kModePlain, true>(*pick, a, (int)grid, st)
+             : launch_cfg<kModePlain, false>(*pick, a, (int)grid, st);
+}
+
+}  // namespace moe

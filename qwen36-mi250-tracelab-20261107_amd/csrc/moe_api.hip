@@ -3,11 +3,12 @@
 // live in route_sort.hip, stream_gemm.hip and combine.hip.
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
 
 #include <string>
 
 #include "../../include/moe_mi355x.h"
-#include "stream_gemm.h"
+#include "expert_gemm.h"
 
 namespace moe {
 hipError_t launch_route(const uint16_t* logits, long long ld, int T, int E, int k, long long* idx64,
@@ -27,7 +28,16 @@ using namespace moe;
 
 namespace {
 
-constexpr int kBM = 64;  // token rows per tile of the streaming GEMM (16 * TOKB)
+// Sorted rows per tile of the expert GEMM: one 16-row MFMA block per tile for decode-sized
+// batches (K split over 4 waves), four blocks above (4 row groups share the staged tokens).
+int tile_rows_for(int T) {
+  const char* env = getenv("MOE_TILE_ROWS");
+  if (env) {
+    int v = atoi(env);
+    if (v == 16 || v == 32 || v == 64 || v == 128) return v;
+  }
+  return T <= 16 ? 16 : (T <= 512 ? 32 : 64);
+}
 
 thread_local std::string g_err;
 
@@ -130,7 +140,7 @@ GemmOperand down_operand(const void* down, const float* scale, int H, int I, con
 
 int run_gate_up(const void* x, int T, int H, int E, int k, int I, const void* gate_up,
                 const float* gu_scale, int wdtype, const void* sh_gate, const void* sh_up, int IS,
-                const int* order, const int* table, int MT, void* act, void* act_sh,
+                const int* order, const int* table, int MT, int bm, void* act, void* act_sh,
                 hipStream_t s) {
   GemmArgs a{};
   a.op[0] = gate_up_operand(gate_up, gu_scale, H, I, x, act);
@@ -157,7 +167,7 @@ int run_gate_up(const void* x, int T, int H, int E, int k, int I, const void* ga
   a.P = T * k;
   a.E = E;
   a.T = T;
-  hipError_t err = launch_stream_gemm(kModeSwiglu, kRoleGateUp, a, MT, s);
+  hipError_t err = launch_expert_gemm(kModeSwiglu, kRoleGateUp, bm, a, MT, s);
   if (err == hipErrorInvalidValue)
     return fail(MOE_EINVAL, "gate_up: no kernel configuration for H=%d I=%d IS=%d", H, I, IS);
   return hip_check(err, "gate_up launch");
@@ -165,7 +175,8 @@ int run_gate_up(const void* x, int T, int H, int E, int k, int I, const void* ga
 
 int run_down(const void* act, int T, int H, int E, int k, int I, const void* down,
              const float* dn_scale, int wdtype, const void* sh_down, int IS, const void* act_sh,
-             const int* order, const int* table, int MT, void* y, void* y_sh, hipStream_t s) {
+             const int* order, const int* table, int MT, int bm, void* y, void* y_sh,
+             hipStream_t s) {
   GemmArgs a{};
   a.op[0] = down_operand(down, dn_scale, H, I, act, y);
   a.op[0].fp8 = wdtype == MOE_WEIGHTS_FP8_E4M3;
@@ -190,7 +201,7 @@ int run_down(const void* act, int T, int H, int E, int k, int I, const void* dow
   a.P = T * k;
   a.E = E;
   a.T = T;
-  hipError_t err = launch_stream_gemm(kModePlain, kRoleDown, a, MT, s);
+  hipError_t err = launch_expert_gemm(kModePlain, kRoleDown, bm, a, MT, s);
   if (err == hipErrorInvalidValue)
     return fail(MOE_EINVAL, "down: no kernel configuration for H=%d I=%d IS=%d", H, I, IS);
   return hip_check(err, "down launch");
@@ -204,7 +215,7 @@ int moe_abi_version(void) { return 1; }
 
 const char* moe_last_error(void) { return g_err.c_str(); }
 
-int moe_tile_rows(void) { return kBM; }
+int moe_tile_rows(int T) { return tile_rows_for(T); }
 
 int moe_max_tiles(int T, int k, int E, int bm, int has_shared) {
   if (T < 0 || k < 1 || E < 1 || bm < 1) return 0;
@@ -235,8 +246,9 @@ int moe_router_logits(const void* x, int T, int H, const void* w_pack, int n_pac
   a.P = 0;
   a.E = 0;
   a.T = T;
-  int mt = (T + kBM - 1) / kBM;
-  hipError_t err = launch_stream_gemm(kModePlain, kRoleRouter, a, mt, (hipStream_t)stream);
+  const int bm = tile_rows_for(T);
+  int mt = (T + bm - 1) / bm;
+  hipError_t err = launch_expert_gemm(kModePlain, kRoleRouter, bm, a, mt, (hipStream_t)stream);
   if (err == hipErrorInvalidValue) return fail(MOE_EINVAL, "router: no configuration for H=%d", H);
   return hip_check(err, "router launch");
 }
@@ -271,8 +283,8 @@ int moe_sort(const long long* idx64, int T, int k, int E, int bm, int has_shared
 
 int moe_grouped_gate_up(const void* x, int T, int H, int E, int k, int I, const void* gate_up,
                         const float* gu_scale, int wdtype, const int* order, const int* table,
-                        int max_tiles, void* act, const void* sh_gate, const void* sh_up, int IS,
-                        void* act_sh, void* stream) {
+                        int max_tiles, int bm, void* act, const void* sh_gate, const void* sh_up,
+                        int IS, void* act_sh, void* stream) {
   int rc = check_experts_shape(T, H, E, k, I);
   if (rc) return rc;
   CHECK_ARG(wdtype == MOE_WEIGHTS_BF16 || (wdtype == MOE_WEIGHTS_FP8_E4M3 && gu_scale),
@@ -282,14 +294,15 @@ int moe_grouped_gate_up(const void* x, int T, int H, int E, int k, int I, const 
                          (((intptr_t)sh_up - (intptr_t)sh_gate) & 1) == 0),
             "shared expert needs sh_up, act_sh and IS a multiple of 32");
   if (T == 0) return MOE_OK;
+  CHECK_ARG(bm == 16 || bm == 32 || bm == 64 || bm == 128, "bm must be 16, 32, 64 or 128 (got %d)", bm);
   return run_gate_up(x, T, H, E, k, I, gate_up, gu_scale, wdtype, sh_gate, sh_up, IS, order,
-                     table, max_tiles, act, act_sh, (hipStream_t)stream);
+                     table, max_tiles, bm, act, act_sh, (hipStream_t)stream);
 }
 
 int moe_grouped_down(const void* act, int T, int H, int E, int k, int I, const void* down,
                      const float* dn_scale, int wdtype, const int* order, const int* table,
-                     int max_tiles, void* y, const void* sh_down, int IS, const void* act_sh,
-                     void* y_sh, void* stream) {
+                     int max_tiles, int bm, void* y, const void* sh_down, int IS,
+                     const void* act_sh, void* y_sh, void* stream) {
   int rc = check_experts_shape(T, H, E, k, I);
   if (rc) return rc;
   CHECK_ARG(wdtype == MOE_WEIGHTS_BF16 || (wdtype == MOE_WEIGHTS_FP8_E4M3 && dn_scale),
@@ -298,8 +311,9 @@ int moe_grouped_down(const void* act, int T, int H, int E, int k, int I, const v
   CHECK_ARG(!sh_down || (act_sh && y_sh && IS >= 32 && IS % 32 == 0),
             "shared expert needs act_sh, y_sh and IS a multiple of 32");
   if (T == 0) return MOE_OK;
+  CHECK_ARG(bm == 16 || bm == 32 || bm == 64 || bm == 128, "bm must be 16, 32, 64 or 128 (got %d)", bm);
   return run_down(act, T, H, E, k, I, down, dn_scale, wdtype, sh_down, IS, act_sh, order, table,
-                  max_tiles, y, y_sh, (hipStream_t)stream);
+                  max_tiles, bm, y, y_sh, (hipStream_t)stream);
 }
 
 int moe_combine(const void* y, const void* w, int T, int H, int k, const void* ysh,
@@ -324,13 +338,14 @@ struct ExpertsWs {
   int *idx32, *counts, *offsets, *order, *table, *scratch;
   uint16_t *act, *y;
   size_t bytes;
-  int MT;
+  int MT, bm;
 };
 ExpertsWs carve_experts(void* base, int T, int H, int E, int k, int I) {
   Carver c{static_cast<char*>(base)};
   ExpertsWs w{};
   const int P = T * k;
-  w.MT = max_tiles_of(T, k, E, kBM, 0);
+  w.bm = tile_rows_for(T);
+  w.MT = max_tiles_of(T, k, E, w.bm, 0);
   w.counts = c.take<int>(E);
   w.offsets = c.take<int>(E);
   w.order = c.take<int>(P);
@@ -365,14 +380,14 @@ int moe_experts_forward(const void* x, int T, int H, int E, int k, int I,
   CHECK_ARG(workspace && workspace_bytes >= w.bytes, "workspace too small: %zu < %zu",
             workspace_bytes, w.bytes);
   hipStream_t s = (hipStream_t)stream;
-  HIP_TRY(launch_route_sort(nullptr, 0, nullptr, top_k_index, T, E, k, kBM, 0, nullptr, nullptr,
+  HIP_TRY(launch_route_sort(nullptr, 0, nullptr, top_k_index, T, E, k, w.bm, 0, nullptr, nullptr,
                             nullptr, w.counts, w.offsets, w.order, w.table, w.MT, w.scratch, s),
           "sort launch");
   rc = run_gate_up(x, T, H, E, k, I, gate_up, gu_scale, wdtype, nullptr, nullptr, 0, w.order,
-                   w.table, w.MT, w.act, nullptr, s);
+                   w.table, w.MT, w.bm, w.act, nullptr, s);
   if (rc) return rc;
   rc = run_down(w.act, T, H, E, k, I, down, dn_scale, wdtype, nullptr, 0, nullptr, w.order, w.table,
-                w.MT, w.y, nullptr, s);
+                w.MT, w.bm, w.y, nullptr, s);
   if (rc) return rc;
   return hip_check(launch_combine(w.y, static_cast<const uint16_t*>(top_k_weights), k, nullptr,
                                   nullptr, 0, nullptr, static_cast<uint16_t*>(out), T, H,
@@ -391,13 +406,14 @@ struct BlockWs {
   int *counts, *offsets, *order, *table, *scratch;
   uint16_t *act, *act_sh, *y, *y_sh;
   size_t bytes;
-  int MT;
+  int MT, bm;
 };
 BlockWs carve_block(void* base, int T, int H, int E, int k, int I, int IS, int n_pack) {
   Carver c{static_cast<char*>(base)};
   BlockWs w{};
   const int P = T * k;
-  w.MT = max_tiles_of(T, k, E, kBM, 1);
+  w.bm = tile_rows_for(T);
+  w.MT = max_tiles_of(T, k, E, w.bm, 1);
   w.logits = c.take<uint16_t>((size_t)T * n_pack);
   w.idx64 = c.take<long long>(P);
   w.idx32 = c.take<int>(P);
@@ -447,14 +463,14 @@ int moe_block_forward(const void* x, int T, int H, int E, int k, int I, int IS,
   uint16_t* wt = top_k_weights ? static_cast<uint16_t*>(top_k_weights) : w.w;
   rc = moe_router_logits(x, T, H, w_pack, n_pack, lg, stream);
   if (rc) return rc;
-  HIP_TRY(launch_route_sort(lg, n_pack, nullptr, nullptr, T, E, k, kBM, 1, i64, w.idx32, wt,
+  HIP_TRY(launch_route_sort(lg, n_pack, nullptr, nullptr, T, E, k, w.bm, 1, i64, w.idx32, wt,
                             w.counts, w.offsets, w.order, w.table, w.MT, w.scratch, s),
           "route/sort launch");
   rc = run_gate_up(x, T, H, E, k, I, gate_up, gu_scale, wdtype, sh_gate, sh_up, IS, w.order,
-                   w.table, w.MT, w.act, w.act_sh, s);
+                   w.table, w.MT, w.bm, w.act, w.act_sh, s);
   if (rc) return rc;
   rc = run_down(w.act, T, H, E, k, I, down, dn_scale, wdtype, sh_down, IS, w.act_sh, w.order,
-                w.table, w.MT, w.y, w.y_sh, s);
+                w.table, w.MT, w.bm, w.y, w.y_sh, s);
   if (rc) return rc;
   return hip_check(launch_combine(w.y, wt, k, w.y_sh, lg + E, n_pack,
                                   static_cast<const uint16_t*>(residual),

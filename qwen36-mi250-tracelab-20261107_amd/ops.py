@@ -140,7 +140,7 @@ def sort_pairs(top_k_index: torch.Tensor, experts: int, bm: int | None = None,
     idx = top_k_index.contiguous()
     tokens, top_k = idx.shape
     lib = _lib.load()
-    bm = lib.moe_tile_rows() if bm is None else bm
+    bm = lib.moe_tile_rows(tokens) if bm is None else bm
     max_tiles = lib.moe_max_tiles(tokens, top_k, experts, bm, int(shared))
     dev = idx.device
     counts = torch.empty(experts, dtype=torch.int32, device=dev)
@@ -163,8 +163,6 @@ def grouped_gate_up(x: torch.Tensor, top_k: int, gate_up: torch.Tensor, sp: Sort
     x = _bf16(x, "x")
     w, s, wd = expert_weight(gate_up, scale, "gate_up")
     _check_row_major(w)
-    if sp.bm != _lib.load().moe_tile_rows():
-        raise ValueError("the grouped GEMM needs a table built with the default tile rows")
     tokens, hidden = x.shape
     experts, two_i, _ = w.shape
     inter = two_i // 2
@@ -177,8 +175,9 @@ def grouped_gate_up(x: torch.Tensor, top_k: int, gate_up: torch.Tensor, sp: Sort
         act_sh = torch.empty((tokens, inter_s), dtype=torch.bfloat16, device=x.device)
     lib = _lib.load()
     check(lib.moe_grouped_gate_up(ptr(x), tokens, hidden, experts, top_k, inter, ptr(w), ptr(s), wd,
-                                  ptr(sp.order), ptr(sp.table), sp.max_tiles, ptr(act), ptr(sg),
-                                  ptr(su), inter_s, ptr(act_sh), stream_of(x)), "grouped_gate_up")
+                                  ptr(sp.order), ptr(sp.table), sp.max_tiles, sp.bm, ptr(act),
+                                  ptr(sg), ptr(su), inter_s, ptr(act_sh), stream_of(x)),
+          "grouped_gate_up")
     return act if shared is None else (act, act_sh)
 
 
@@ -200,8 +199,9 @@ def grouped_down(act: torch.Tensor, tokens: int, top_k: int, down: torch.Tensor,
         y_sh = torch.empty((tokens, hidden), dtype=torch.bfloat16, device=act.device)
     lib = _lib.load()
     check(lib.moe_grouped_down(ptr(act), tokens, hidden, experts, top_k, inter, ptr(w), ptr(s), wd,
-                               ptr(sp.order), ptr(sp.table), sp.max_tiles, ptr(y), ptr(sd),
-                               inter_s, ptr(act_sh), ptr(y_sh), stream_of(act)), "grouped_down")
+                               ptr(sp.order), ptr(sp.table), sp.max_tiles, sp.bm, ptr(y),
+                               ptr(sd), inter_s, ptr(act_sh), ptr(y_sh), stream_of(act)),
+          "grouped_down")
     return y if shared is None else (y, y_sh)
 
 
