@@ -57,7 +57,8 @@ def make_layer(torch, dev, seed, zipf=False, fp8=False):
     if zipf:
         from oracle import moe_oracle as orc  # noqa: PLC0415 - synthetic-input construction only
 
-        r, v = orc.zipf_router(router.cpu(), s=1.1, mu=4.0, seed=seed)
+        r, v = orc.zipf_router(router.cpu(), seed=seed)
+        v = v * orc.ZIPF_MU
         router = r.to(dev)
         v = v.to(dev)
     gu, dn = rnd(E, 2 * I, H), rnd(E, H, I)
@@ -146,7 +147,7 @@ def run_config(torch, dev, name, T, layers, steps, warmup, zipf=False, fp8=False
         g = torch.Generator(device=dev).manual_seed(li + 7)
         x = torch.randn(T, H, generator=g, device=dev)
         if v is not None:
-            x = x + 4.0 * v[None, :]
+            x = x + v[None, :]  # v already scaled by the Zipf construction's mu
         mlps.append(mlp)
         xs.append(x.to(torch.bfloat16))
         pkg.block.pack_router(mlp)

@@ -39,11 +39,19 @@ struct GemmArgs {
   const int* order;  // sorted row -> pair
   int topk, P, E, T;
   int nrb;           // weight-row blocks per tile (set by the launcher)
+  int dbg;           // 0; tuning experiments only (MOE_GEMM_DEBUG): 1 skip token-row
+                     // loads, 2 skip MFMAs, 4 skip per-chunk barriers
 };
 
-// Launches k_expert_gemm over max_tiles tiles of at most bm (16, 32 or 64) sorted rows.
+// Launches k_expert_gemm over max_tiles tiles of at most bm (16, 32, 64 or 128) sorted rows.
+// Both operands of one launch must have the same weight type.
 // hipErrorInvalidValue: no kernel configuration fits the operands' shapes.
 hipError_t launch_expert_gemm(int mode, int role, int bm, const GemmArgs& a, int max_tiles,
                               hipStream_t st);
+
+// Prefill tiles (prefill_gemm.hip): 256 sorted rows x 256 weight rows per workgroup, bf16.
+int prefill_tile_rows();
+bool prefill_fits(int mode, const GemmOperand& op);
+hipError_t launch_prefill_gemm(int mode, const GemmArgs& a, int max_tiles, hipStream_t st);
 
 }  // namespace moe

@@ -86,7 +86,7 @@ __global__ __launch_bounds__(64 * WR * WK) void k_expert_gemm(GemmArgs args) {
   const int kbeg = wk * Kw;
   const int nch = Kw / KC;
   const int ntb = (r1 - r0 + 15) >> 4;
-  const bool use_fp8 = HAS_FP8 && op.fp8;
+  constexpr bool use_fp8 = HAS_FP8;  // a launch is all-fp8 or all-bf16
 
   // ---- A operand: this lane's weight row, first NA chunks requested at once.
   long long wrow_off;
@@ -208,8 +208,13 @@ __global__ __launch_bounds__(64 * WR * WK) void k_expert_gemm(GemmArgs args) {
 #pragma unroll
               for (int h = 0; h < 2; ++h) b[s2 * 2 + h] = brow[s2 * 8 + kq * 2 + h];
           }
+          if (!(args.dbg & 2)) {
 #pragma unroll
-          for (int s = 0; s < LPC16; ++s) acc[tb] = mfma16x16x32(a4[s], b[s], acc[tb]);
+            for (int s = 0; s < LPC16; ++s) acc[tb] = mfma16x16x32(a4[s], b[s], acc[tb]);
+          } else {
+#pragma unroll
+            for (int s = 0; s < LPC16; ++s) acc[tb][0] += __uint_as_float(a4[s].x ^ b[s].y);
+          }
         }
       }
       // next chunk's token rows into the other LDS buffer
@@ -229,12 +234,12 @@ __global__ __launch_bounds__(64 * WR * WK) void k_expert_gemm(GemmArgs args) {
           for (int s = 0; s < LPC8; ++s) aring[cc][s] = ld16(wp8 + (c + R) * KC + s * 64);
         }
       }
-      if (c + 1 + R < nch) {
+      if (c + 1 + R < nch && !(args.dbg & 1)) {
 #pragma unroll
         for (int i = 0; i < STG; ++i)
           if (sneed[i]) bring[(cc + 1) % R][i] = ld16(xin + srow[i] + (c + 1 + R) * KC);
       }
-      __syncthreads();
+      if (!(args.dbg & 4)) __syncthreads();
     }
   }
 
@@ -306,34 +311,44 @@ __global__ __launch_bounds__(64 * WR * WK) void k_expert_gemm(GemmArgs args) {
 namespace {
 
 struct Cfg {
-  int wr, wk, tokb, kc;
+  int wr, wk, tokb, kc, r = 4;  // r: chunks in flight
 };
 
 template <int MODE, bool HAS_FP8>
 hipError_t launch_cfg(const Cfg& c, const GemmArgs& a, int grid, hipStream_t st) {
-#define MOE_L(WR, WK, TOKB, KCV)                                                                \
-  if (c.wr == WR && c.wk == WK && c.tokb == TOKB && c.kc == KCV) {                              \
-    hipLaunchKernelGGL((k_expert_gemm<MODE, WR, WK, TOKB, HAS_FP8, KCV>), dim3(grid),           \
+#define MOE_L(WR, WK, TOKB, KCV, RV)                                                            \
+  if (c.wr == WR && c.wk == WK && c.tokb == TOKB && c.kc == KCV && c.r == RV) {                 \
+    hipLaunchKernelGGL((k_expert_gemm<MODE, WR, WK, TOKB, HAS_FP8, KCV, RV>), dim3(grid),       \
                        dim3(64 * WR * WK), 0, st, a);                                           \
     return hipGetLastError();                                                                   \
   }
-  MOE_L(1, 4, 1, 128)
-  MOE_L(1, 2, 1, 128)
-  MOE_L(1, 1, 1, 128)
-  MOE_L(4, 1, 4, 128)
-  MOE_L(4, 1, 1, 128)
-  MOE_L(2, 2, 2, 128)
-  MOE_L(2, 1, 2, 128)
-  MOE_L(1, 4, 1, 64)
-  MOE_L(4, 1, 4, 64)
-  MOE_L(2, 2, 2, 64)
-  MOE_L(2, 1, 2, 64)
-  MOE_L(4, 1, 8, 64)
-  MOE_L(2, 1, 8, 64)
-  if constexpr (!HAS_FP8) {
-    MOE_L(1, 1, 1, 32)
-    MOE_L(1, 1, 2, 32)
-    MOE_L(1, 1, 4, 32)
+  if constexpr (HAS_FP8) {
+    MOE_L(1, 4, 1, 64, 8)
+    MOE_L(2, 2, 2, 64, 8)
+    MOE_L(2, 1, 2, 64, 8)
+    MOE_L(4, 1, 4, 64, 8)
+    MOE_L(1, 4, 1, 128, 4)
+    MOE_L(2, 2, 2, 128, 4)
+    MOE_L(2, 1, 2, 128, 4)
+    MOE_L(4, 1, 4, 128, 4)
+    MOE_L(1, 2, 1, 128, 4)
+    MOE_L(1, 1, 1, 128, 4)
+    MOE_L(4, 1, 8, 64, 4)
+  } else {
+    MOE_L(1, 4, 1, 64, 4)
+    MOE_L(2, 2, 2, 64, 4)
+    MOE_L(2, 1, 2, 64, 4)
+    MOE_L(4, 1, 4, 64, 4)
+    MOE_L(4, 1, 8, 64, 4)
+    MOE_L(1, 2, 1, 128, 4)
+    MOE_L(1, 1, 1, 128, 4)
+    MOE_L(1, 4, 1, 128, 4)
+    MOE_L(2, 2, 2, 128, 4)
+    MOE_L(2, 1, 2, 128, 4)
+    MOE_L(4, 1, 4, 128, 4)
+    MOE_L(1, 1, 1, 32, 4)
+    MOE_L(1, 1, 2, 32, 4)
+    MOE_L(1, 1, 4, 32, 4)
   }
 #undef MOE_L
   return hipErrorInvalidConfiguration;
@@ -356,7 +371,8 @@ bool env_cfg(int role, Cfg* out) {
   if (!p) return false;
   Cfg c{};
   c.kc = 128;
-  if (sscanf(p + strlen(names[role]), "%d,%d,%d", &c.wr, &c.wk, &c.kc) < 2) return false;
+  c.r = 4;
+  if (sscanf(p + strlen(names[role]), "%d,%d,%d,%d", &c.wr, &c.wk, &c.kc, &c.r) < 2) return false;
   *out = c;
   return true;
 }
@@ -366,7 +382,11 @@ bool env_cfg(int role, Cfg* out) {
 hipError_t launch_expert_gemm(int mode, int role, int bm, const GemmArgs& a_in, int max_tiles,
                               hipStream_t st) {
   GemmArgs a = a_in;
+  if (const char* dbg = getenv("MOE_GEMM_DEBUG"))
+    if (role != kRoleRouter) a.dbg = atoi(dbg);
   const bool fp8 = (a.op[0].N > 0 && a.op[0].fp8) || (a.op[1].N > 0 && a.op[1].fp8);
+  if (a.op[0].N > 0 && a.op[1].N > 0 && a.op[0].fp8 != a.op[1].fp8)
+    return hipErrorInvalidValue;  // one weight type per launch (the caller splits)
   const int tokb = bm / 16;
   if (bm % 16 || (tokb != 1 && tokb != 2 && tokb != 4 && tokb != 8)) return hipErrorInvalidValue;
   // Preferences: with one 16-token block per tile, split K over 4 waves (more waves for the
@@ -379,38 +399,43 @@ hipError_t launch_expert_gemm(int mode, int role, int bm, const GemmArgs& a_in, 
     prefs[n++] = forced;
   }
   (void)0;
+  // fp8 weights move half the bytes per K element: 128-element chunks keep as many bytes
+  // in flight as the bf16 64-element ones.
+  const int rr = fp8 ? 8 : 4;  // fp8: 64-element chunks are half the bytes, twice as many
   if (tokb == 1) {
-    prefs[n++] = {1, 4, 1, 64};
+    prefs[n++] = {1, 4, 1, 64, rr};
     prefs[n++] = {1, 2, 1, 128};
     prefs[n++] = {1, 1, 1, 128};
   } else if (tokb == 2) {
-    prefs[n++] = role == kRoleDown ? Cfg{2, 1, 2, 64} : Cfg{2, 2, 2, 64};
-    prefs[n++] = {2, 1, 2, 64};
+    prefs[n++] = role == kRoleDown ? Cfg{2, 1, 2, 64, rr} : Cfg{2, 2, 2, 64, rr};
+    prefs[n++] = {2, 1, 2, 128};
   } else if (tokb == 4) {
-    prefs[n++] = {4, 1, 4, 64};
+    prefs[n++] = {4, 1, 4, 64, rr};
   } else {
     prefs[n++] = {4, 1, 8, 64};
   }
   prefs[n++] = {1, 1, tokb, 32};  // small test shapes (K a multiple of 32)
-  const Cfg* pick = nullptr;
-  for (int i = 0; i < n; ++i)
-    if (fits(prefs[i], mode, a.op[0]) && fits(prefs[i], mode, a.op[1]) &&
-        prefs[i].wk * 2 * prefs[i].tokb * 16 * (prefs[i].kc / 8 + 1) * 16 <= 65536) {
-      pick = &prefs[i];
-      break;
-    }
-  if (!pick) return hipErrorInvalidValue;
-  int rows = (mode == kModeSwiglu ? 8 : 16) * pick->wr;
-  int nmax = a.op[0].N > a.op[1].N ? a.op[0].N : a.op[1].N;
-  a.nrb = nmax / rows;
-  if (a.nrb <= 0 || max_tiles <= 0) return hipSuccess;
-  long long grid = (long long)max_tiles * a.nrb;
-  if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
-  if (mode == kModeSwiglu)
-    return fp8 ? launch_cfg<kModeSwiglu, true>(*pick, a, (int)grid, st)
-               : launch_cfg<kModeSwiglu, false>(*pick, a, (int)grid, st);
-  return fp8 ? launch_cfg<kModePlain, true>(*pick, a, (int)grid, st)
-             : launch_cfg<kModePlain, false>(*pick, a, (int)grid, st);
+  for (int i = 0; i < n; ++i) {
+    const Cfg& c = prefs[i];
+    if (!fits(c, mode, a.op[0]) || !fits(c, mode, a.op[1])) continue;
+    if (c.wk * 2 * c.tokb * 16 * (c.kc / 8 + 1) * 16 > 65536) continue;
+    int rows = (mode == kModeSwiglu ? 8 : 16) * c.wr;
+    int nmax = a.op[0].N > a.op[1].N ? a.op[0].N : a.op[1].N;
+    a.nrb = nmax / rows;
+    if (a.nrb <= 0 || max_tiles <= 0) return hipSuccess;
+    long long grid = (long long)max_tiles * a.nrb;
+    if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
+    hipError_t err;
+    if (mode == kModeSwiglu)
+      err = fp8 ? launch_cfg<kModeSwiglu, true>(c, a, (int)grid, st)
+                : launch_cfg<kModeSwiglu, false>(c, a, (int)grid, st);
+    else
+      err = fp8 ? launch_cfg<kModePlain, true>(c, a, (int)grid, st)
+                : launch_cfg<kModePlain, false>(c, a, (int)grid, st);
+    if (err == hipErrorInvalidConfiguration) continue;  // not instantiated: next choice
+    return err;
+  }
+  return hipErrorInvalidValue;
 }
 
 }  // namespace moe

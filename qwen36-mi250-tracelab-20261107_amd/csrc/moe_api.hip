@@ -28,15 +28,20 @@ using namespace moe;
 
 namespace {
 
-// Sorted rows per tile of the expert GEMM: one 16-row MFMA block per tile for decode-sized
-// batches (K split over 4 waves), four blocks above (4 row groups share the staged tokens).
-int tile_rows_for(int T) {
+// Sorted rows per tile of the grouped GEMMs: one 16-row MFMA block for decode-sized batches
+// (K split over 4 waves), two blocks up to 512 tokens, and 256-row tiles of the prefill
+// kernel above (bf16 weights with shapes it tiles; else 64-row tiles of the expert GEMM).
+int tile_rows_for(int T, bool fp8 = false, int H = 2048, int I = 512, int IS = 512) {
   const char* env = getenv("MOE_TILE_ROWS");
   if (env) {
     int v = atoi(env);
-    if (v == 16 || v == 32 || v == 64 || v == 128) return v;
+    if (v == 16 || v == 32 || v == 64 || v == 128 || v == 256) return v;
   }
-  return T <= 16 ? 16 : (T <= 512 ? 32 : 64);
+  if (T <= 16) return 16;
+  if (T <= 512) return 32;
+  const bool prefill_ok = !fp8 && H % 256 == 0 && I % 128 == 0 && IS % 128 == 0 &&
+                          H % 64 == 0 && I % 64 == 0 && IS % 64 == 0;
+  return prefill_ok ? 256 : 64;
 }
 
 thread_local std::string g_err;
@@ -138,6 +143,23 @@ GemmOperand down_operand(const void* down, const float* scale, int H, int I, con
   return o;
 }
 
+// One launch for the routed experts and the shared expert, or two when their weight types
+// differ (fp8 experts, bf16 shared expert): the shared expert's tiles then come from the
+// token count alone (rows P .. P + T), not from the table.
+hipError_t launch_split(int mode, int role, int bm, const GemmArgs& a, int MT, hipStream_t s) {
+  if (a.op[0].N <= 0 || a.op[1].N <= 0 || a.op[0].fp8 == a.op[1].fp8)
+    return launch_expert_gemm(mode, role, bm, a, MT, s);
+  GemmArgs r = a;
+  r.op[1].N = 0;
+  hipError_t err = launch_expert_gemm(mode, role, bm, r, MT, s);
+  if (err != hipSuccess) return err;
+  GemmArgs v = a;
+  v.op[0] = v.op[1];
+  v.op[0].N = 0;
+  v.table = nullptr;
+  return launch_expert_gemm(mode, role, bm, v, (a.T + bm - 1) / bm, s);
+}
+
 int run_gate_up(const void* x, int T, int H, int E, int k, int I, const void* gate_up,
                 const float* gu_scale, int wdtype, const void* sh_gate, const void* sh_up, int IS,
                 const int* order, const int* table, int MT, int bm, void* act, void* act_sh,
@@ -167,7 +189,8 @@ int run_gate_up(const void* x, int T, int H, int E, int k, int I, const void* ga
   a.P = T * k;
   a.E = E;
   a.T = T;
-  hipError_t err = launch_expert_gemm(kModeSwiglu, kRoleGateUp, bm, a, MT, s);
+  hipError_t err = bm == prefill_tile_rows() ? launch_prefill_gemm(kModeSwiglu, a, MT, s)
+                                             : launch_split(kModeSwiglu, kRoleGateUp, bm, a, MT, s);
   if (err == hipErrorInvalidValue)
     return fail(MOE_EINVAL, "gate_up: no kernel configuration for H=%d I=%d IS=%d", H, I, IS);
   return hip_check(err, "gate_up launch");
@@ -201,7 +224,8 @@ int run_down(const void* act, int T, int H, int E, int k, int I, const void* dow
   a.P = T * k;
   a.E = E;
   a.T = T;
-  hipError_t err = launch_expert_gemm(kModePlain, kRoleDown, bm, a, MT, s);
+  hipError_t err = bm == prefill_tile_rows() ? launch_prefill_gemm(kModePlain, a, MT, s)
+                                             : launch_split(kModePlain, kRoleDown, bm, a, MT, s);
   if (err == hipErrorInvalidValue)
     return fail(MOE_EINVAL, "down: no kernel configuration for H=%d I=%d IS=%d", H, I, IS);
   return hip_check(err, "down launch");
@@ -246,7 +270,8 @@ int moe_router_logits(const void* x, int T, int H, const void* w_pack, int n_pac
   a.P = 0;
   a.E = 0;
   a.T = T;
-  const int bm = tile_rows_for(T);
+  // 16-token tiles with K split over 4 waves: the most waves for a 1 MiB weight.
+  const int bm = 16;
   int mt = (T + bm - 1) / bm;
   hipError_t err = launch_expert_gemm(kModePlain, kRoleRouter, bm, a, mt, (hipStream_t)stream);
   if (err == hipErrorInvalidValue) return fail(MOE_EINVAL, "router: no configuration for H=%d", H);
@@ -294,7 +319,8 @@ int moe_grouped_gate_up(const void* x, int T, int H, int E, int k, int I, const 
                          (((intptr_t)sh_up - (intptr_t)sh_gate) & 1) == 0),
             "shared expert needs sh_up, act_sh and IS a multiple of 32");
   if (T == 0) return MOE_OK;
-  CHECK_ARG(bm == 16 || bm == 32 || bm == 64 || bm == 128, "bm must be 16, 32, 64 or 128 (got %d)", bm);
+  CHECK_ARG(bm == 16 || bm == 32 || bm == 64 || bm == 128 || bm == 256,
+            "bm must be 16, 32, 64, 128 or 256 (got %d)", bm);
   return run_gate_up(x, T, H, E, k, I, gate_up, gu_scale, wdtype, sh_gate, sh_up, IS, order,
                      table, max_tiles, bm, act, act_sh, (hipStream_t)stream);
 }
@@ -311,7 +337,8 @@ int moe_grouped_down(const void* act, int T, int H, int E, int k, int I, const v
   CHECK_ARG(!sh_down || (act_sh && y_sh && IS >= 32 && IS % 32 == 0),
             "shared expert needs act_sh, y_sh and IS a multiple of 32");
   if (T == 0) return MOE_OK;
-  CHECK_ARG(bm == 16 || bm == 32 || bm == 64 || bm == 128, "bm must be 16, 32, 64 or 128 (got %d)", bm);
+  CHECK_ARG(bm == 16 || bm == 32 || bm == 64 || bm == 128 || bm == 256,
+            "bm must be 16, 32, 64, 128 or 256 (got %d)", bm);
   return run_down(act, T, H, E, k, I, down, dn_scale, wdtype, sh_down, IS, act_sh, order, table,
                   max_tiles, bm, y, y_sh, (hipStream_t)stream);
 }
@@ -340,11 +367,11 @@ struct ExpertsWs {
   size_t bytes;
   int MT, bm;
 };
-ExpertsWs carve_experts(void* base, int T, int H, int E, int k, int I) {
+ExpertsWs carve_experts(void* base, int T, int H, int E, int k, int I, bool fp8) {
   Carver c{static_cast<char*>(base)};
   ExpertsWs w{};
   const int P = T * k;
-  w.bm = tile_rows_for(T);
+  w.bm = tile_rows_for(T, fp8, H, I, I);
   w.MT = max_tiles_of(T, k, E, w.bm, 0);
   w.counts = c.take<int>(E);
   w.offsets = c.take<int>(E);
@@ -360,7 +387,10 @@ ExpertsWs carve_experts(void* base, int T, int H, int E, int k, int I) {
 
 size_t moe_experts_workspace_bytes(int T, int H, int E, int k, int I) {
   if (T < 0 || k < 1 || E < 1) return 0;
-  return carve_experts(nullptr, T, H, E, k, I).bytes;
+  // the fp8 plan never needs more workspace than the bf16 one
+  size_t a = carve_experts(nullptr, T, H, E, k, I, false).bytes;
+  size_t b = carve_experts(nullptr, T, H, E, k, I, true).bytes;
+  return a > b ? a : b;
 }
 
 int moe_experts_forward(const void* x, int T, int H, int E, int k, int I,
@@ -376,7 +406,7 @@ int moe_experts_forward(const void* x, int T, int H, int E, int k, int I,
             "bad weight dtype / missing scales");
   CHECK_ARG(x && top_k_index && top_k_weights && gate_up && down && out, "null pointer");
   if (T == 0) return MOE_OK;
-  ExpertsWs w = carve_experts(workspace, T, H, E, k, I);
+  ExpertsWs w = carve_experts(workspace, T, H, E, k, I, wdtype == MOE_WEIGHTS_FP8_E4M3);
   CHECK_ARG(workspace && workspace_bytes >= w.bytes, "workspace too small: %zu < %zu",
             workspace_bytes, w.bytes);
   hipStream_t s = (hipStream_t)stream;
@@ -408,11 +438,12 @@ struct BlockWs {
   size_t bytes;
   int MT, bm;
 };
-BlockWs carve_block(void* base, int T, int H, int E, int k, int I, int IS, int n_pack) {
+BlockWs carve_block(void* base, int T, int H, int E, int k, int I, int IS, int n_pack,
+                    bool fp8) {
   Carver c{static_cast<char*>(base)};
   BlockWs w{};
   const int P = T * k;
-  w.bm = tile_rows_for(T);
+  w.bm = tile_rows_for(T, fp8, H, I, IS);
   w.MT = max_tiles_of(T, k, E, w.bm, 1);
   w.logits = c.take<uint16_t>((size_t)T * n_pack);
   w.idx64 = c.take<long long>(P);
@@ -434,7 +465,9 @@ BlockWs carve_block(void* base, int T, int H, int E, int k, int I, int IS, int n
 
 size_t moe_block_workspace_bytes(int T, int H, int E, int k, int I, int IS, int n_pack) {
   if (T < 0 || k < 1 || E < 1) return 0;
-  return carve_block(nullptr, T, H, E, k, I, IS, n_pack).bytes;
+  size_t a = carve_block(nullptr, T, H, E, k, I, IS, n_pack, false).bytes;
+  size_t b = carve_block(nullptr, T, H, E, k, I, IS, n_pack, true).bytes;
+  return a > b ? a : b;
 }
 
 int moe_block_forward(const void* x, int T, int H, int E, int k, int I, int IS,
@@ -454,7 +487,7 @@ int moe_block_forward(const void* x, int T, int H, int E, int k, int I, int IS,
   CHECK_ARG(x && w_pack && gate_up && down && sh_gate && sh_up && sh_down && out, "null pointer");
   CHECK_ARG((((intptr_t)sh_up - (intptr_t)sh_gate) & 1) == 0, "misaligned shared weights");
   if (T == 0) return MOE_OK;
-  BlockWs w = carve_block(workspace, T, H, E, k, I, IS, n_pack);
+  BlockWs w = carve_block(workspace, T, H, E, k, I, IS, n_pack, wdtype == MOE_WEIGHTS_FP8_E4M3);
   CHECK_ARG(workspace && workspace_bytes >= w.bytes, "workspace too small: %zu < %zu",
             workspace_bytes, w.bytes);
   hipStream_t s = (hipStream_t)stream;

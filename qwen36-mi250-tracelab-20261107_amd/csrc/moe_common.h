@@ -47,10 +47,12 @@ __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) {
 }
 
 // 16 OCP e4m3fn bytes -> two bf16x8 operands (exact: every e4m3 value is a bf16 value).
+// gfx950's scaled conversion with scale 1.0 turns two e4m3 bytes into two bf16 in one step.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 template <bool HI>
 __device__ __forceinline__ uint32_t fp8x2_to_bf16x2(uint32_t w) {
-  auto f = __builtin_amdgcn_cvt_pk_f32_fp8(w, HI);
-  return __builtin_amdgcn_perm(__float_as_uint(f[1]), __float_as_uint(f[0]), 0x07060302u);
+  bf16x2_t r = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, HI);
+  return __builtin_bit_cast(uint32_t, r);
 }
 __device__ __forceinline__ void fp8x16_to_bf16(uint4 q, uint4& lo, uint4& hi) {
   lo.x = fp8x2_to_bf16x2<false>(q.x);

@@ -130,6 +130,28 @@ def test_experts_forward_matches_oracle(pkg, dev, n, mode, shape):
     assert torch.equal(got, again), "not deterministic"
 
 
+@pytest.mark.parametrize("n", [600, 1500])
+@pytest.mark.parametrize("mode", ["uniform", "skewed", "one"])
+def test_experts_prefill_tiles_match_oracle(pkg, dev, n, mode):
+    """More than 512 tokens: the 256-row prefill GEMM tiles (H % 256 == 0, I % 128 == 0)."""
+    e, h, i, k = 32, 256, 128, 8
+    _say("experts prefill", n, mode)
+    assert pkg._lib.load().moe_tile_rows(n) == 256
+    m = _Experts(e, h, i, seed=n)
+    g = torch.Generator().manual_seed(n + 2)
+    x = torch.randn(n, h, generator=g).to(BF16)
+    idx, w = routing(n, e, k, mode, g)
+    gpu = _Experts(e, h, i, seed=n)
+    gpu.gate_up_proj, gpu.down_proj = m.gate_up_proj.to(dev), m.down_proj.to(dev)
+    got = pkg.experts.experts_forward(gpu, x.to(dev), idx.to(dev), w.to(dev))
+    again = pkg.experts.experts_forward(gpu, x.to(dev), idx.to(dev), w.to(dev))
+    torch.cuda.synchronize()
+    ref = orc.sorted_experts(x, idx, w, m.gate_up_proj, m.down_proj)
+    scale = max(1.0, ref.float().abs().max().item())
+    assert max_abs(got, ref) <= TOL * scale
+    assert torch.equal(got, again), "not deterministic"
+
+
 @pytest.mark.parametrize("n", [3, 40])
 def test_grouped_stages_match_oracle(pkg, dev, n):
     """gate_up -> act (sorted rows) and down -> y (pair rows) separately."""
@@ -202,7 +224,7 @@ def _full_weights(dev, seed=0, zipf=False):
     }
     v = None
     if zipf:
-        r, v = orc.zipf_router(w["router"].cpu(), s=1.1, mu=4.0, seed=seed)
+        r, v = orc.zipf_router(w["router"].cpu(), seed=seed)
         w["router"] = r.to(dev)
     return w, v
 
@@ -238,6 +260,28 @@ def test_block_full_shape(pkg, dev, full_layer, T):
     assert max_abs(out, f32) <= 2e-2
     assert max_abs(out, ref) <= 2e-2
     assert ours <= max(5e-3, 1.1 * theirs)
+
+
+@pytest.mark.parametrize("T", [1024, 4096])
+def test_block_full_shape_prefill(pkg, dev, full_layer, T):
+    """Prefill-sized chunks of the full layer (the C4 path): routing bit-exact for every
+    token given the logits; values against the fp32 oracle on 64 sampled tokens (each
+    token's output depends on that token alone)."""
+    _say("block full prefill", T)
+    w, _ = full_layer
+    g = torch.Generator().manual_seed(T)
+    x = torch.randn(T, 2048, generator=g).to(BF16)
+    out, idx, wts, logits = pkg.block.moe(x.to(dev), _gpu_mlp(w, dev), 8, return_routing=True)
+    torch.cuda.synchronize()
+    lg = logits.cpu()[:, :256]
+    _, ref_i = orc.route(lg, 8)
+    assert torch.equal(idx.cpu(), ref_i)
+    pick = torch.randperm(T, generator=g)[:64]
+    f32 = orc.block_fp32(x[pick], w, ref_i[pick], logits=lg[pick])
+    o = out.cpu()[pick]
+    _say(f" vs fp32 on 64 tokens: max {max_abs(o, f32):.3g} mean-rel {mean_rel(o, f32):.3g}")
+    assert max_abs(o, f32) <= 2e-2 and mean_rel(o, f32) <= 6e-3
+    assert torch.isfinite(out.float()).all()
 
 
 def test_block_residual(pkg, dev):

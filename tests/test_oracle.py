@@ -262,3 +262,17 @@ def test_fp8_row_quantisation_error_bound():
     rel = (deq - w.float()).abs() / w.float().abs().amax(-1, keepdim=True)
     assert rel.max() <= 2.0 ** -4 / 448 * 448 * 0.5 + 1e-6 or rel.max() <= 1 / 16
     assert (q.float().abs().amax(-1) == 448).all()
+
+
+def test_zipf_router_distinct_experts():
+    """C3's skewed routing: 64 tokens x top-8 touch ~140 distinct experts, as Zipf(1.1)
+    sampling without replacement does (5-95%: 131-151), and popularity is rank-ordered."""
+    g = torch.Generator().manual_seed(0)
+    router = (torch.randn(256, 2048, generator=g) * 0.02).to(BF16)
+    ds = []
+    for seed in range(3):
+        w, v = orc.zipf_router(router, seed=seed)
+        x = (torch.randn(64, 2048, generator=g) + orc.ZIPF_MU * v).to(BF16)
+        _, idx = orc.route(F.linear(x, w), 8)
+        ds.append(int(torch.unique(idx).numel()))
+    assert all(115 <= d <= 165 for d in ds), ds
