@@ -3,6 +3,10 @@
  * Plain device pointers, sizes and a hipStream_t passed as void*. No entry point
  * allocates device memory or synchronises with the host: callers pass a workspace of
  * moe_*_workspace_bytes(...) bytes, so every call can be captured in a HIP graph.
+ * Workspace contract: its first MOE_SYNC_BYTES bytes hold arrival counters of the fused
+ * kernel tails; they must be zero before the first call that uses the workspace, and
+ * every call leaves them zero. Calls that share a workspace must not overlap (use one
+ * workspace per stream).
  * All tensors are contiguous row-major. bf16 tensors are passed as raw 16-bit words.
  * fp8 weights are OCP e4m3fn bytes with one fp32 scale per output row.
  *
@@ -25,6 +29,8 @@
 #ifdef __cplusplus
 extern "C" {
 #endif
+
+#define MOE_SYNC_BYTES 4096
 
 #define MOE_OK 0
 #define MOE_EINVAL 1

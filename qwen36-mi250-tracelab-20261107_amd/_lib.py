@@ -103,3 +103,24 @@ def ptr(t) -> int | None:
 def stream_of(t) -> int:
     """The current HIP stream of ``t``'s device, as the C ABI's ``void* stream``."""
     return torch.cuda.current_stream(t.device).cuda_stream
+
+
+SYNC_BYTES = 4096  # the workspace head the fused kernels use as arrival counters
+
+_WORKSPACES: dict = {}
+
+
+def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """A workspace of at least ``nbytes`` for calls on ``device``'s current stream.
+
+    One workspace is kept per (device, stream) and reused: its first ``SYNC_BYTES`` must be
+    zero before a call and every call leaves them zero (zeroed once at allocation, by a
+    fill kernel). Calls on one stream run in order, so they never share it concurrently."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    key = (idx, torch.cuda.current_stream(device).cuda_stream)
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() < nbytes:
+        size = max(nbytes, SYNC_BYTES, 0 if ws is None else 2 * ws.numel())
+        ws = torch.zeros(size, dtype=torch.uint8, device=device)
+        _WORKSPACES[key] = ws
+    return ws

@@ -123,11 +123,12 @@ def moe(x: torch.Tensor, mlp, top_k: int, decode: bool = False,
     if tokens:
         lib = _lib.load()
         nbytes = lib.moe_block_workspace_bytes(tokens, hidden, experts, top_k, inter, inter_s, n_pack)
-        ws = torch.empty(nbytes, dtype=torch.uint8, device=x2.device)
+        ws = _lib.workspace(x2.device, nbytes)
         check(lib.moe_block_forward(
             ptr(x2), tokens, hidden, experts, top_k, inter, inter_s, ptr(pack), n_pack, ptr(gu),
             ptr(gus), ptr(dn), ptr(dns), wd, ptr(sg), ptr(su), ptr(sd), ptr(residual), mode,
-            ptr(out), ptr(idx), ptr(wts), ptr(logits), ptr(ws), nbytes, stream_of(x2)), "moe block")
+            ptr(out), ptr(idx), ptr(wts), ptr(logits), ptr(ws), ws.numel(), stream_of(x2)),
+            "moe block")
     out = out.reshape(shape)
     if return_routing:
         return out, idx, wts, logits

@@ -20,53 +20,7 @@ __global__ __launch_bounds__(256) void k_combine(
   const int t = blockIdx.x / nb;
   const int c = ((blockIdx.x - t * nb) * blockDim.x + threadIdx.x) * 8;
   if (t >= T || c >= H) return;
-  float acc[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) acc[i] = 0.f;
-  for (int j = 0; j < k; ++j) {
-    long long p = (long long)t * k + j;
-    float wj = bf_bits2f(w[p]);
-    uint4 v = ld16(y + p * H + c);
-    uint32_t u[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float a = bf_lo(u[i]) * wj, b = bf_hi(u[i]) * wj;
-      if (round_w) {
-        a = rbf(a);
-        b = rbf(b);
-      }
-      acc[2 * i] += a;
-      acc[2 * i + 1] += b;
-    }
-  }
-  float o[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) o[i] = rbf(acc[i]);
-  if (ysh) {
-    float g = rbf(sigmoidf_(bf_bits2f(seg[(long long)t * ld_seg])));
-    uint4 v = ld16(ysh + (long long)t * H + c);
-    uint32_t u[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      o[2 * i] = rbf(o[2 * i] + rbf(g * bf_lo(u[i])));
-      o[2 * i + 1] = rbf(o[2 * i + 1] + rbf(g * bf_hi(u[i])));
-    }
-  }
-  if (res) {
-    uint4 v = ld16(res + (long long)t * H + c);
-    uint32_t u[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      o[2 * i] = o[2 * i] + bf_lo(u[i]);
-      o[2 * i + 1] = o[2 * i + 1] + bf_hi(u[i]);
-    }
-  }
-  uint4 r;
-  r.x = pack_bf2(o[0], o[1]);
-  r.y = pack_bf2(o[2], o[3]);
-  r.z = pack_bf2(o[4], o[5]);
-  r.w = pack_bf2(o[6], o[7]);
-  st16(out + (long long)t * H + c, r);
+  combine8(y, w, k, ysh, seg, ld_seg, res, out, t, H, c, round_w);
 }
 
 hipError_t launch_combine(const uint16_t* y, const uint16_t* w, int k, const uint16_t* ysh,

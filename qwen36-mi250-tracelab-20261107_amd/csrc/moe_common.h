@@ -69,6 +69,76 @@ __device__ __forceinline__ f32x4_t mfma16x16x32(uint4 a, uint4 b, f32x4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
 }
 
+// Weighted combine of 8 consecutive columns c..c+7 of token t (see combine.hip):
+//   bf16(bf16(sum_j term(y[t*k+j], w[t*k+j])) + bf16(bf16(sigmoid(seg_t)) * ysh[t]))
+//   (+ residual), term = bf16(y*w) when round_w else y*w (exact in fp32).
+__device__ __forceinline__ void combine8(const uint16_t* __restrict__ y,
+                                         const uint16_t* __restrict__ w, int k,
+                                         const uint16_t* __restrict__ ysh,
+                                         const uint16_t* __restrict__ seg, long long ld_seg,
+                                         const uint16_t* __restrict__ res,
+                                         uint16_t* __restrict__ out, int t, int H, int c,
+                                         int round_w) {
+  float acc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc[i] = 0.f;
+  // Pairs in groups of 8 whose loads are all issued before the first is used: one memory
+  // round trip per group instead of one per pair.
+  for (int j0 = 0; j0 < k; j0 += 8) {
+    uint4 v[8];
+    float wj[8];
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) {
+      const long long p = (long long)t * k + min(j0 + jj, k - 1);
+      v[jj] = ld16(y + p * H + c);
+      wj[jj] = bf_bits2f(w[p]);
+    }
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) {
+      if (j0 + jj >= k) break;
+      uint32_t u[4] = {v[jj].x, v[jj].y, v[jj].z, v[jj].w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float a = bf_lo(u[i]) * wj[jj], b = bf_hi(u[i]) * wj[jj];
+        if (round_w) {
+          a = rbf(a);
+          b = rbf(b);
+        }
+        acc[2 * i] += a;
+        acc[2 * i + 1] += b;
+      }
+    }
+  }
+  float o[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) o[i] = rbf(acc[i]);
+  if (ysh) {
+    float g = rbf(sigmoidf_(bf_bits2f(seg[(long long)t * ld_seg])));
+    uint4 v = ld16(ysh + (long long)t * H + c);
+    uint32_t u[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      o[2 * i] = rbf(o[2 * i] + rbf(g * bf_lo(u[i])));
+      o[2 * i + 1] = rbf(o[2 * i + 1] + rbf(g * bf_hi(u[i])));
+    }
+  }
+  if (res) {
+    uint4 v = ld16(res + (long long)t * H + c);
+    uint32_t u[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      o[2 * i] = o[2 * i] + bf_lo(u[i]);
+      o[2 * i + 1] = o[2 * i + 1] + bf_hi(u[i]);
+    }
+  }
+  uint4 r;
+  r.x = pack_bf2(o[0], o[1]);
+  r.y = pack_bf2(o[2], o[3]);
+  r.z = pack_bf2(o[4], o[5]);
+  r.w = pack_bf2(o[6], o[7]);
+  st16(out + (long long)t * H + c, r);
+}
+
 // Tile table layout (shared with the host): for max_tiles MT,
 //   table[t] = expert, table[MT + t] = first sorted row, table[2 MT + t] = row end,
 //   table[3 MT] = number of tiles.

@@ -16,108 +16,11 @@
 // row, row end per BM-row tile; the tile count at 3 * max_tiles), plus optional
 // "shared expert" tiles appended after the routed ones: expert id E, rows P + j*BM
 // up to P + T (the shared expert sees every token).
-#include "moe_common.h"
+#include "route_sort_dev.h"
 
 namespace moe {
 
-constexpr int kSortThreads = 1024;
-constexpr int kSortWaves = kSortThreads / kWave;
-constexpr int kSmallMaxPairs = 4096;
-constexpr int kSmallMaxE = 512;
-constexpr int kMaxE = 1024;
-
 // ---------------------------------------------------------------------------- routing
-
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
-  return v;
-}
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
-  return v;
-}
-
-// One wave routes one row of E bf16 logits. Lane l owns experts l, l+64, ...
-// Writes (for lanes j < k) sel_idx / sel_w of pick j through the callback arrays.
-template <int EPL>
-__device__ void route_row(const uint16_t* __restrict__ lrow, int E, int k, int lane,
-                          int& my_idx, float& my_w) {
-  float p[EPL];
-  float m = -INFINITY;
-#pragma unroll
-  for (int i = 0; i < EPL; ++i) {
-    int e = lane + kWave * i;
-    float z = e < E ? bf_bits2f(lrow[e]) : -INFINITY;
-    p[i] = z;
-    m = fmaxf(m, z);
-  }
-  m = wave_max(m);
-  float s = 0.f;
-#pragma unroll
-  for (int i = 0; i < EPL; ++i) {
-    int e = lane + kWave * i;
-    p[i] = e < E ? expf(p[i] - m) : 0.f;
-    s += p[i];
-  }
-  s = wave_sum(s);
-#pragma unroll
-  for (int i = 0; i < EPL; ++i) {
-    int e = lane + kWave * i;
-    p[i] = e < E ? p[i] / s : -1.0f;
-  }
-  float tot = 0.f;
-  float mine_p = 0.f;
-  int mine_i = 0;
-  for (int j = 0; j < k; ++j) {
-    float bp = -2.0f;
-    int bi = 0x7fffffff;
-#pragma unroll
-    for (int i = 0; i < EPL; ++i)
-      if (p[i] > bp) {  // strict: the lowest expert of the lane wins a tie
-        bp = p[i];
-        bi = lane + kWave * i;
-      }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-      float op = __shfl_xor(bp, off);
-      int oi = __shfl_xor(bi, off);
-      if (op > bp || (op == bp && oi < bi)) {
-        bp = op;
-        bi = oi;
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < EPL; ++i)
-      if (lane + kWave * i == bi) p[i] = -1.0f;
-    tot += bp;  // sequential j order
-    if (lane == j) {
-      mine_p = bp;
-      mine_i = bi;
-    }
-  }
-  my_idx = mine_i;
-  my_w = mine_p / tot;
-}
-
-template <int EPL>
-__device__ void route_rows(const uint16_t* __restrict__ logits, long long ld, int t, int E, int k,
-                           int lane, long long* __restrict__ idx64, int* __restrict__ idx32,
-                           uint16_t* __restrict__ w_out, int* __restrict__ keys_lds,
-                           int* __restrict__ counts_g) {
-  int my_i;
-  float my_w;
-  route_row<EPL>(logits + (long long)t * ld, E, k, lane, my_i, my_w);
-  if (lane < k) {
-    long long pidx = (long long)t * k + lane;
-    if (idx64) idx64[pidx] = my_i;
-    if (idx32) idx32[pidx] = my_i;
-    if (w_out) w_out[pidx] = f2bf_bits(my_w);
-    if (keys_lds) keys_lds[pidx] = my_i;
-    if (counts_g) atomicAdd(counts_g + my_i, 1);
-  }
-}
 
 template <int EPL>
 __global__ __launch_bounds__(256) void k_route(const uint16_t* __restrict__ logits, long long ld,
@@ -130,93 +33,8 @@ __global__ __launch_bounds__(256) void k_route(const uint16_t* __restrict__ logi
   route_rows<EPL>(logits, ld, t, E, k, lane, idx64, idx32, w_out, nullptr, counts);
 }
 
-// ------------------------------------------------------------------ block-level helpers
-
-// Exclusive scan of one int per thread over the whole block (<= 1024 threads).
-__device__ int block_excl_scan(int v, int* tmp, int& total) {
-  int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
-  int x = v;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    int y = __shfl_up(x, off);
-    if (lane >= off) x += y;
-  }
-  if (lane == 63) tmp[w] = x;
-  __syncthreads();
-  if (w == 0) {
-    int t = lane < nw ? tmp[lane] : 0;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      int y = __shfl_up(t, off);
-      if (lane >= off) t += y;
-    }
-    if (lane < nw) tmp[lane] = t;
-  }
-  __syncthreads();
-  int base = w > 0 ? tmp[w - 1] : 0;
-  total = tmp[nw - 1];
-  __syncthreads();
-  return base + x - v;
-}
-
-// From per-expert counts in LDS: global counts / offsets, the offsets in LDS, and the
-// tile table. Requires E <= blockDim.x.
-__device__ void build_table(const int* cnt, int E, int P, int T, int bm, int has_shared,
-                            int* offs_lds, int* __restrict__ counts_g, int* __restrict__ offsets_g,
-                            int* __restrict__ table, int MT, int* tmp) {
-  int e = threadIdx.x;
-  int c = e < E ? cnt[e] : 0;
-  int total;
-  int st = block_excl_scan(c, tmp, total);
-  int nt = (c + bm - 1) / bm;
-  int ntot;
-  int tst = block_excl_scan(nt, tmp, ntot);
-  if (e < E) {
-    offs_lds[e] = st;
-    if (counts_g) counts_g[e] = c;
-    if (offsets_g) offsets_g[e] = st;
-    for (int j = 0; j < nt; ++j) {
-      int t = tst + j;
-      table[t] = e;
-      table[MT + t] = st + j * bm;
-      table[2 * MT + t] = st + c;
-    }
-  }
-  int nsh = has_shared ? (T + bm - 1) / bm : 0;
-  for (int j = threadIdx.x; j < nsh; j += blockDim.x) {
-    int t = ntot + j;
-    table[t] = E;
-    table[MT + t] = P + j * bm;
-    table[2 * MT + t] = P + T;
-  }
-  if (threadIdx.x == 0) table[3 * MT] = ntot + nsh;
-  __syncthreads();
-}
-
-// Stable in-block ranks: thread i holds key (valid when valid). Returns the number of
-// valid keys equal to key at lower thread ids of the block. wcnt is [waves][E] in LDS.
-__device__ int block_stable_rank(int key, bool valid, int E, int nbits, int* wcnt) {
-  int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
-  for (int i = threadIdx.x; i < nw * E; i += blockDim.x) wcnt[i] = 0;
-  __syncthreads();
-  unsigned long long m = __ballot(valid);
-  for (int b = 0; b < nbits; ++b) {
-    bool bit = (key >> b) & 1;
-    unsigned long long bb = __ballot(bit);
-    m &= bit ? bb : ~bb;
-  }
-  int rank = __popcll(m & ((1ull << lane) - 1ull));
-  if (valid && rank == 0) wcnt[w * E + key] = __popcll(m);
-  __syncthreads();
-  if (valid)
-    for (int v = 0; v < w; ++v) rank += wcnt[v * E + key];
-  return rank;
-}
-
 // ------------------------------------------------------------------- small fused path
 
-// One workgroup: (optionally) route T rows, then count, scan, build the tile table
-// and scatter the stable order. P = T * k <= kSmallMaxPairs, E <= kSmallMaxE.
 template <int EPL>
 __global__ __launch_bounds__(kSortThreads) void k_route_sort_small(
     const uint16_t* __restrict__ logits, long long ld, const int* __restrict__ ids32_in,
@@ -224,42 +42,9 @@ __global__ __launch_bounds__(kSortThreads) void k_route_sort_small(
     long long* __restrict__ idx64, int* __restrict__ idx32, uint16_t* __restrict__ w_out,
     int* __restrict__ counts_g, int* __restrict__ offsets_g, int* __restrict__ order,
     int* __restrict__ table, int MT) {
-  __shared__ int keys[kSmallMaxPairs];
-  __shared__ int hist[kSmallMaxE];
-  __shared__ int offs[kSmallMaxE];
-  __shared__ int wcnt[kSortWaves * kSmallMaxE];
-  __shared__ int tmp[kSortWaves + 1];
-  const int P = T * k;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  for (int e = threadIdx.x; e < E; e += blockDim.x) hist[e] = 0;
-  if (logits) {
-    for (int t = wave; t < T; t += kSortWaves)
-      route_rows<EPL>(logits, ld, t, E, k, lane, idx64, idx32, w_out, keys, nullptr);
-  } else {
-    for (int p = threadIdx.x; p < P; p += blockDim.x) {
-      long long v = ids64_in ? ids64_in[p] : (long long)ids32_in[p];
-      keys[p] = (int)(v < 0 ? 0 : (v >= E ? E - 1 : v));  // clamp as batched_mm does
-    }
-  }
-  __syncthreads();
-  for (int p = threadIdx.x; p < P; p += blockDim.x) atomicAdd(&hist[keys[p]], 1);
-  __syncthreads();
-  build_table(hist, E, P, T, bm, has_shared, offs, counts_g, offsets_g, table, MT, tmp);
-  const int nbits = E > 1 ? 32 - __clz(E - 1) : 1;
-  for (int c0 = 0; c0 < P; c0 += blockDim.x) {
-    int p = c0 + threadIdx.x;
-    bool valid = p < P;
-    int key = valid ? keys[p] : 0;
-    int rank = block_stable_rank(key, valid, E, nbits, wcnt);
-    if (valid) order[offs[key] + rank] = p;
-    __syncthreads();
-    for (int e = threadIdx.x; e < E; e += blockDim.x) {
-      int s = 0;
-      for (int v = 0; v < kSortWaves; ++v) s += wcnt[v * E + e];
-      offs[e] += s;
-    }
-    __syncthreads();
-  }
+  __shared__ SortLds L;
+  route_sort_block<EPL>(logits, ld, ids32_in, ids64_in, T, E, k, bm, has_shared, idx64, idx32,
+                        w_out, counts_g, offsets_g, order, table, MT, L);
 }
 
 // -------------------------------------------------------------------- multi-block path
@@ -328,21 +113,6 @@ __global__ __launch_bounds__(kSortThreads) void k_sort_scatter(const int* __rest
 
 // ---------------------------------------------------------------------- host launchers
 
-#define MOE_EPL_DISPATCH(E, FN)       \
-  do {                                \
-    if ((E) <= 64) {                  \
-      FN(1);                          \
-    } else if ((E) <= 128) {          \
-      FN(2);                          \
-    } else if ((E) <= 256) {          \
-      FN(4);                          \
-    } else if ((E) <= 512) {          \
-      FN(8);                          \
-    } else {                          \
-      FN(16);                         \
-    }                                 \
-  } while (0)
-
 hipError_t launch_route(const uint16_t* logits, long long ld, int T, int E, int k, long long* idx64,
                         int* idx32, uint16_t* w_out, int* counts, hipStream_t s) {
   if (T <= 0) return hipSuccess;
@@ -370,8 +140,12 @@ hipError_t launch_route_sort(const uint16_t* logits, long long ld, const int* id
                              hipStream_t s) {
   const int P = T * k;
   if (sort_uses_small(P, E)) {
+    // one workgroup; a few tokens need few waves (fewer barriers to wait at)
+    int need = P > E ? P : E;
+    int threads = T > 16 ? kSortThreads : ((need + 63) / 64) * 64;
+    if (threads > kSortThreads) threads = kSortThreads;
 #define L(EPL)                                                                                 \
-  hipLaunchKernelGGL(k_route_sort_small<EPL>, dim3(1), dim3(kSortThreads), 0, s, logits, ld,  \
+  hipLaunchKernelGGL(k_route_sort_small<EPL>, dim3(1), dim3(threads), 0, s, logits, ld,       \
                      ids32_in, ids64_in, T, E, k, bm, has_shared, idx64, idx32, w_out, counts, \
                      offsets, order, table, MT)
     MOE_EPL_DISPATCH(E, L);

@@ -261,11 +261,11 @@ def experts(x: torch.Tensor, top_k_index: torch.Tensor, top_k_weights: torch.Ten
         return out
     lib = _lib.load()
     nbytes = lib.moe_experts_workspace_bytes(tokens, hidden, nexp, top_k, inter)
-    ws = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
+    ws = _lib.workspace(x.device, nbytes)
     mode = _lib.ROUND_PRODUCT if round_products else _lib.EXACT_PRODUCT
     check(lib.moe_experts_forward(ptr(x), tokens, hidden, nexp, top_k, inter, ptr(idx), ptr(wts),
                                   ptr(gu), ptr(gus), ptr(dn), ptr(dns), wd, mode, ptr(out), ptr(ws),
-                                  nbytes, stream_of(x)), "experts")
+                                  ws.numel(), stream_of(x)), "experts")
     return out
 
 

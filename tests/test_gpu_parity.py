@@ -296,3 +296,19 @@ def test_block_residual(pkg, dev):
     torch.cuda.synchronize()
     want = (r.float() + a.cpu().float()).to(BF16)
     assert torch.equal(b.cpu(), want)
+
+
+def test_fused_tails_leave_sync_area_zero(pkg, dev, full_layer):
+    """The fused route/sort and combine tails reset their arrival counters: after calls of
+    every regime the workspace head is zero again, and repeated calls give the same bits."""
+    w, _ = full_layer
+    mlp = _gpu_mlp(w, dev)
+    g = torch.Generator().manual_seed(5)
+    for T in (1, 16, 64, 300):
+        x = torch.randn(T, 2048, generator=g).to(BF16).to(dev)
+        a = pkg.block.moe(x, mlp, 8)
+        b = pkg.block.moe(x, mlp, 8)
+        torch.cuda.synchronize()
+        assert torch.equal(a, b), T
+    for ws in pkg._lib._WORKSPACES.values():
+        assert int(ws[: pkg._lib.SYNC_BYTES].count_nonzero()) == 0
