@@ -302,7 +302,7 @@ def main():
         "hbm_TBps": head["layer_TBps"],
         "hbm_frac": head["layer_hbm_frac"],
         "tokens_per_s": head["tokens_per_s"],
-        "roofline": {"bound": "hbm", "kernel": "grouped gate_up (k_stream_gemm SWIGLU)",
+        "roofline": {"bound": "hbm", "kernel": "grouped gate_up (k_expert_gemm SWIGLU)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
                      "bytes_per_launch": kbytes, "us_per_launch": kus},

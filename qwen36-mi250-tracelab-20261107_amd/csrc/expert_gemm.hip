@@ -372,6 +372,8 @@ hipError_t launch_cfg(const Cfg& c, const GemmArgs& a, int grid, hipStream_t st)
     MOE_LAUNCH(WR, WK, TOKB, KCV, RV, (MODE == kModePlain ? FU : 0))                            \
   }
   if constexpr (HAS_FP8) {
+    MOE_L(4, 1, 2, 256, 2)
+    MOE_L(4, 1, 2, 128, 4)
     MOE_L(1, 4, 1, 64, 8)
     MOE_L(2, 2, 2, 64, 8)
     MOE_L(2, 1, 2, 64, 8)
@@ -471,7 +473,14 @@ hipError_t launch_expert_gemm(int mode, int role, int bm, const GemmArgs& a_in, 
     prefs[n++] = {1, 2, 1, 128};
     prefs[n++] = {1, 1, 1, 128};
   } else if (tokb == 2) {
-    prefs[n++] = role == kRoleDown ? Cfg{2, 1, 2, 64, rr} : Cfg{2, 2, 2, 64, rr};
+    if (fp8) {
+      // fp8 32-token tiles: four row groups per workgroup, 256-element chunks, two-deep
+      // ring (fastest of the fp8 configurations measured at the 40-layer T=32 shape)
+      prefs[n++] = {4, 1, 2, 256, 2};
+      prefs[n++] = {4, 1, 2, 128, 4};
+    } else {
+      prefs[n++] = role == kRoleDown ? Cfg{2, 1, 2, 64, rr} : Cfg{2, 2, 2, 64, rr};
+    }
     prefs[n++] = {2, 1, 2, 128};
   } else if (tokb == 4) {
     prefs[n++] = {4, 1, 4, 64, rr};
