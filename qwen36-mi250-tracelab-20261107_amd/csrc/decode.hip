@@ -1,0 +1,430 @@
+// Decode-sized MoE block (T <= 4 tokens) on gfx950 in three launches
+// (subsystems a1, a2, a4, a5, a6, a7, a10, a12 for decode batches).
+//
+// Same results contract as the tiled path (router -> route/sort -> grouped gate_up ->
+// grouped down -> combine; engine/fast/fused.py:887-932, engine/fast/kernels.py:88-164,
+// engine/fast/model.py:1139-1179), with the work regrouped for a handful of tokens, where
+// every weight byte is used by at most four tokens and the block is bound by HBM latency
+// and bandwidth rather than by any arithmetic:
+//
+//   K1 k_dec_router   one wave per router row (logits[t, n] = bf16(x_t . Wpack[n])) and one
+//                     wave per shared-expert gate/up row pair (act_sh = SwiGLU). The shared
+//                     expert does not depend on the routing, so its 4 MiB stream overlaps the
+//                     router's HBM round trip instead of following it.
+//   K2 k_dec_gate_up  every workgroup recomputes the softmax / top-k of the T tokens from the
+//                     logits (a few hundred cycles; it replaces the route + sort launch),
+//                     numbers the distinct experts in first-use order, takes one of them and
+//                     four gate/up row pairs of it, and writes act[pair, n].
+//   K3 k_dec_down     one wave per hidden row n: y_p = bf16(act_p . Wd[e_p, n]) for every
+//                     pair, the shared expert's row, and the combine of those values in the
+//                     routing order j, gated shared term and residual, written straight to out.
+//
+// Every projection is a dot product over a whole weight row: lane l holds elements
+// [512 c + 8 l, 512 c + 8 l + 8) of chunk c, so one load instruction reads 1 KiB (bf16) or
+// 512 B (fp8) of one row contiguously; partial sums are reduced with DPP in a fixed order.
+// Rounding points are those of the tiled kernels (rbf after each projection, SwiGLU as
+// bf16(bf16(silu(bf16 g)) * bf16 u), combine terms bf16(w * y) under round_w).
+#include "moe_common.h"
+#include "route_sort_dev.h"
+#include "decode.h"
+
+namespace moe {
+
+namespace {
+
+constexpr int kDecThreads = 256;  // K2 / K3: four waves, one row (pair) each
+
+__device__ __forceinline__ float dot8(uint4 w, uint4 x, float acc) {
+  acc = fmaf(bf_lo(w.x), bf_lo(x.x), acc);
+  acc = fmaf(bf_hi(w.x), bf_hi(x.x), acc);
+  acc = fmaf(bf_lo(w.y), bf_lo(x.y), acc);
+  acc = fmaf(bf_hi(w.y), bf_hi(x.y), acc);
+  acc = fmaf(bf_lo(w.z), bf_lo(x.z), acc);
+  acc = fmaf(bf_hi(w.z), bf_hi(x.z), acc);
+  acc = fmaf(bf_lo(w.w), bf_lo(x.w), acc);
+  acc = fmaf(bf_hi(w.w), bf_hi(x.w), acc);
+  return acc;
+}
+
+template <bool FP8>
+__device__ __forceinline__ const void* wrow(const void* base, long long row, int K) {
+  return FP8 ? static_cast<const void*>(static_cast<const uint8_t*>(base) + row * K)
+             : static_cast<const void*>(static_cast<const uint16_t*>(base) + row * K);
+}
+
+// Raw (undecoded) weight fragment, so that the loads of a whole row are issued before the
+// first conversion.
+template <bool FP8>
+struct WFrag {
+  uint4 v;
+};
+template <bool FP8>
+__device__ __forceinline__ WFrag<FP8> ldraw(const void* row, int elem) {
+  WFrag<FP8> f;
+  if (FP8) {
+    uint2 q = *reinterpret_cast<const uint2*>(static_cast<const uint8_t*>(row) + elem);
+    f.v = make_uint4(q.x, q.y, 0u, 0u);
+  } else {
+    f.v = ld16(static_cast<const uint16_t*>(row) + elem);
+  }
+  return f;
+}
+template <bool FP8>
+__device__ __forceinline__ uint4 decode(WFrag<FP8> f) {
+  if (FP8)
+    return make_uint4(fp8x2_to_bf16x2<false>(f.v.x), fp8x2_to_bf16x2<true>(f.v.x),
+                      fp8x2_to_bf16x2<false>(f.v.y), fp8x2_to_bf16x2<true>(f.v.y));
+  return f.v;
+}
+
+__device__ __forceinline__ float swiglu(float g, float u) {
+  return rbf(rbf(siluf_(rbf(g))) * rbf(u));
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------------------- K1
+
+// grid: n_pack + IS (shared rows, when sh_gate) workgroups of one wave. The weight rows are
+// requested before the token rows so that both are in flight together.
+template <int NT, int HC>
+__global__ __launch_bounds__(64) void k_dec_router(DecodeArgs a) {
+  const int lane = threadIdx.x;
+  const int g = blockIdx.x;
+  const int H = HC * 512;
+  const bool router = g < a.n_pack;
+  const int n = g - a.n_pack;  // shared gate/up row pair
+  const uint16_t* r0 = router ? a.w_pack + (long long)g * H : a.sh_gate + (long long)n * H;
+  const uint16_t* r1 = router ? r0 : a.sh_up + (long long)n * H;
+  uint4 w0[HC], w1[HC];
+#pragma unroll
+  for (int c = 0; c < HC; ++c) w0[c] = ld16(r0 + c * 512 + lane * 8);
+  if (!router) {
+#pragma unroll
+    for (int c = 0; c < HC; ++c) w1[c] = ld16(r1 + c * 512 + lane * 8);
+  }
+  uint4 xv[NT][HC];
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int c = 0; c < HC; ++c)
+      xv[t][c] = ld16(a.x + (long long)min(t, a.T - 1) * H + c * 512 + lane * 8);
+  if (router) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      float s = 0.f;
+#pragma unroll
+      for (int c = 0; c < HC; ++c) s = dot8(w0[c], xv[t][c], s);
+      s = wave_sum(s);
+      if (lane == 0 && t < a.T) a.logits[(long long)t * a.n_pack + g] = f2bf_bits(s);
+    }
+    return;
+  }
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    float sg = 0.f, su = 0.f;
+#pragma unroll
+    for (int c = 0; c < HC; ++c) {
+      sg = dot8(w0[c], xv[t][c], sg);
+      su = dot8(w1[c], xv[t][c], su);
+    }
+    sg = wave_sum(sg);
+    su = wave_sum(su);
+    if (lane == 0 && t < a.T) a.act_sh[(long long)t * a.IS + n] = f2bf_bits(swiglu(sg, su));
+  }
+}
+
+// ------------------------------------------------------------------------------- K2
+
+// grid: P slots x (I / 4) row blocks; slots past the number of distinct experts exit.
+template <int NT, int HC, bool FP8, int EPL>
+__global__ __launch_bounds__(kDecThreads) void k_dec_gate_up(DecodeArgs a) {
+  __shared__ int s_idx[64];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int H = HC * 512;
+  const int P = a.T * a.k;
+  const int nrb = a.I / 4;
+  const int slot = blockIdx.x / nrb;
+  const int n = (blockIdx.x - slot * nrb) * 4 + wave;
+
+  // token rows: independent of the routing, requested first
+  uint4 xv[NT][HC];
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int c = 0; c < HC; ++c)
+      xv[t][c] = ld16(a.x + (long long)min(t, a.T - 1) * H + c * 512 + lane * 8);
+
+  if (a.logits) {
+    if (wave < a.T) {
+      int my_idx;
+      float my_w;
+      route_row<EPL>(a.logits + (long long)wave * a.n_pack, a.E, a.k, lane, my_idx, my_w);
+      if (lane < a.k) {
+        const int p = wave * a.k + lane;
+        const uint16_t wb = f2bf_bits(my_w);
+        s_idx[p] = my_idx;
+        if (blockIdx.x == 0) {
+          a.idx32[p] = my_idx;
+          a.wts[p] = wb;
+          if (a.idx64) a.idx64[p] = my_idx;
+        }
+      }
+    }
+  } else if (threadIdx.x < P) {
+    const long long v = a.ids_in[threadIdx.x];
+    const int e = (int)(v < 0 ? 0 : (v >= a.E ? a.E - 1 : v));
+    s_idx[threadIdx.x] = e;
+    if (blockIdx.x == 0) a.idx32[threadIdx.x] = e;
+  }
+  __syncthreads();
+
+  // distinct experts numbered in first-use order (pair order)
+  const int key = lane < P ? s_idx[lane] : -1;
+  bool first = lane < P;
+  for (int q = 0; q < P; ++q) {
+    const int kq = s_idx[q];
+    if (q < lane && kq == key) first = false;
+  }
+  const unsigned long long fmask = __ballot(first);
+  const int rank = __popcll(fmask & ((1ull << lane) - 1ull));
+  if (slot >= __popcll(fmask)) return;
+  const unsigned long long smask = __ballot(first && rank == slot);
+  const int e = __builtin_amdgcn_readlane(key, __ffsll((long long)smask) - 1);
+  unsigned long long pmask = __ballot(lane < P && key == e);  // pairs of this expert
+
+  const long long base = (long long)e * 2 * a.I;
+  const void* rg = wrow<FP8>(a.gate_up, base + n, H);
+  const void* ru = wrow<FP8>(a.gate_up, base + a.I + n, H);
+  WFrag<FP8> fg[HC], fu[HC];
+#pragma unroll
+  for (int c = 0; c < HC; ++c) {
+    fg[c] = ldraw<FP8>(rg, c * 512 + lane * 8);
+    fu[c] = ldraw<FP8>(ru, c * 512 + lane * 8);
+  }
+  float sg[NT], su[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) sg[t] = su[t] = 0.f;
+#pragma unroll
+  for (int c = 0; c < HC; ++c) {
+    const uint4 wg = decode<FP8>(fg[c]);
+    const uint4 wu = decode<FP8>(fu[c]);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      sg[t] = dot8(wg, xv[t][c], sg[t]);
+      su[t] = dot8(wu, xv[t][c], su[t]);
+    }
+  }
+  float scg = 1.f, scu = 1.f;
+  if (a.gu_scale) {
+    scg = a.gu_scale[base + n];
+    scu = a.gu_scale[base + a.I + n];
+  }
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    sg[t] = wave_sum(sg[t]) * scg;
+    su[t] = wave_sum(su[t]) * scu;
+  }
+  // lane 0 writes each pair of this expert (at most one per token)
+  while (pmask) {
+    const int p = __ffsll((long long)pmask) - 1;
+    pmask &= pmask - 1;
+    const int t = p / a.k;
+    float g = sg[0], u = su[0];
+#pragma unroll
+    for (int tt = 1; tt < NT; ++tt)
+      if (t == tt) {
+        g = sg[tt];
+        u = su[tt];
+      }
+    if (lane == 0) a.act[(long long)p * a.I + n] = f2bf_bits(swiglu(g, u));
+  }
+}
+
+// ------------------------------------------------------------------------------- K3
+
+// grid: H / 4 workgroups; wave w computes hidden row 4 * blockIdx.x + w of every token.
+template <int NT, int IC, bool FP8>
+__global__ __launch_bounds__(kDecThreads) void k_dec_down(DecodeArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int I = IC * 512;
+  const int P = a.T * a.k;
+  const int H = a.H;
+  const bool shared = a.sh_down != nullptr;
+  const int isc = a.IS / 512;
+
+  // shared row and the shared activations do not depend on the routing: request them first
+  uint4 ws[2], xs[NT][2];
+  if (shared) {
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+      if (c < isc) ws[c] = ld16(a.sh_down + (long long)n * a.IS + c * 512 + lane * 8);
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+        if (c < isc)
+          xs[t][c] = ld16(a.act_sh + (long long)min(t, a.T - 1) * a.IS + c * 512 + lane * 8);
+  }
+  // routing, shared-gate logit and residual of every token: one round trip together
+  const int kv = lane < P ? a.idx32[lane] : 0;
+  const float wv = lane < P ? bf_bits2f(a.wts[lane]) : 0.f;
+  const int tl = min(lane, a.T - 1);
+  // unconditional loads from always-valid addresses (a predicated load would be waited on
+  // before the branch around it)
+  const uint16_t* segp = shared ? a.logits + (long long)tl * a.n_pack + a.E : a.wts;
+  const uint16_t* resp = a.residual ? a.residual + (long long)tl * H + n : a.wts;
+  const float seg_l = bf_bits2f(*segp);
+  const float res_l = bf_bits2f(*resp);
+
+  float acc[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) acc[t] = 0.f;
+  // pairs in groups of 8: all loads of a group are in flight before the first dot
+  for (int p0 = 0; p0 < P; p0 += 8) {
+    WFrag<FP8> wf[8][IC];
+    uint4 av[8][IC];
+    int ev[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int p = min(p0 + i, P - 1);
+      ev[i] = __builtin_amdgcn_readlane(kv, p);
+      const void* row = wrow<FP8>(a.down, (long long)ev[i] * H + n, I);
+#pragma unroll
+      for (int c = 0; c < IC; ++c) {
+        wf[i][c] = ldraw<FP8>(row, c * 512 + lane * 8);
+        av[i][c] = ld16(a.act + (long long)p * I + c * 512 + lane * 8);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int p = p0 + i;
+      if (p >= P) break;
+      float s = 0.f;
+#pragma unroll
+      for (int c = 0; c < IC; ++c) s = dot8(decode<FP8>(wf[i][c]), av[i][c], s);
+      s = wave_sum(s);
+      if (a.dn_scale) s *= a.dn_scale[(long long)ev[i] * H + n];
+      const float y = rbf(s);
+      const float w = __shfl(wv, p);
+      const float term = a.round_w ? rbf(w * y) : w * y;
+      const int t = p / a.k;  // pairs run token-major, j ascending inside a token
+#pragma unroll
+      for (int tt = 0; tt < NT; ++tt)
+        if (t == tt) acc[tt] += term;
+    }
+  }
+
+  float o[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) o[t] = rbf(acc[t]);
+  if (shared) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      float s = 0.f;
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+        if (c < isc) s = dot8(ws[c], xs[t][c], s);
+      s = wave_sum(s);
+      const float gte = rbf(sigmoidf_(__shfl(seg_l, t)));
+      o[t] = rbf(o[t] + rbf(gte * rbf(s)));
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    if (t >= a.T) break;
+    // lane t holds token t's residual
+    if (lane == t) a.out[(long long)t * H + n] = f2bf_bits(a.residual ? o[t] + res_l : o[t]);
+  }
+}
+
+// ------------------------------------------------------------------------ host side
+
+bool decode_fits(const DecodeArgs& a) {
+  const int P = a.T * a.k;
+  if (a.T < 1 || a.T > kDecMaxTokens || P > 64 || a.k < 1) return false;
+  if (a.H % 512 || a.H > 4096 || a.I % 512 || a.I > 1024 || a.I < 512) return false;
+  if (a.logits && (a.E > 512 || a.E < 1)) return false;
+  if (a.sh_down && (a.IS % 512 || a.IS > 1024 || a.IS < 512)) return false;
+  return true;
+}
+
+namespace {
+
+template <int NT>
+hipError_t launch_router_nt(const DecodeArgs& a, hipStream_t s) {
+  const int grid = a.n_pack + (a.sh_gate ? a.IS : 0);
+  switch (a.H / 512) {
+#define L(HC)                                                                             \
+  case HC:                                                                                \
+    hipLaunchKernelGGL((k_dec_router<NT, HC>), dim3(grid), dim3(64), 0, s, a); \
+    break;
+    L(1) L(2) L(4) L(8)
+#undef L
+    default:
+      return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+template <int NT, bool FP8>
+hipError_t launch_gate_up_nt(const DecodeArgs& a, hipStream_t s) {
+  const int grid = a.T * a.k * (a.I / 4);
+  const int epl = a.logits ? (a.E + 63) / 64 : 1;
+#define LG(HC, EPL)                                                                         \
+  if (a.H / 512 == HC && epl <= EPL) {                                                      \
+    hipLaunchKernelGGL((k_dec_gate_up<NT, HC, FP8, EPL>), dim3(grid), dim3(kDecThreads), 0, s, a); \
+    return hipGetLastError();                                                               \
+  }
+#define LH(HC) LG(HC, 1) LG(HC, 2) LG(HC, 4) LG(HC, 8)
+  LH(1) LH(2) LH(4) LH(8)
+#undef LH
+#undef LG
+  return hipErrorInvalidValue;
+}
+
+template <int NT, bool FP8>
+hipError_t launch_down_nt(const DecodeArgs& a, hipStream_t s) {
+  const int grid = a.H / 4;
+  if (a.I == 512)
+    hipLaunchKernelGGL((k_dec_down<NT, 1, FP8>), dim3(grid), dim3(kDecThreads), 0, s, a);
+  else if (a.I == 1024)
+    hipLaunchKernelGGL((k_dec_down<NT, 2, FP8>), dim3(grid), dim3(kDecThreads), 0, s, a);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_decode_router(const DecodeArgs& a, hipStream_t s) {
+  if (a.T == 1) return launch_router_nt<1>(a, s);
+  if (a.T == 2) return launch_router_nt<2>(a, s);
+  return launch_router_nt<4>(a, s);
+}
+
+hipError_t launch_decode_gate_up(const DecodeArgs& a, hipStream_t s) {
+  if (a.fp8) {
+    if (a.T == 1) return launch_gate_up_nt<1, true>(a, s);
+    if (a.T == 2) return launch_gate_up_nt<2, true>(a, s);
+    return launch_gate_up_nt<4, true>(a, s);
+  }
+  if (a.T == 1) return launch_gate_up_nt<1, false>(a, s);
+  if (a.T == 2) return launch_gate_up_nt<2, false>(a, s);
+  return launch_gate_up_nt<4, false>(a, s);
+}
+
+hipError_t launch_decode_down(const DecodeArgs& a, hipStream_t s) {
+  if (a.fp8) {
+    if (a.T == 1) return launch_down_nt<1, true>(a, s);
+    if (a.T == 2) return launch_down_nt<2, true>(a, s);
+    return launch_down_nt<4, true>(a, s);
+  }
+  if (a.T == 1) return launch_down_nt<1, false>(a, s);
+  if (a.T == 2) return launch_down_nt<2, false>(a, s);
+  return launch_down_nt<4, false>(a, s);
+}
+
+}  // namespace moe

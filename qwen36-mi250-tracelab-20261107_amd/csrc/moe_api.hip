@@ -10,6 +10,7 @@
 
 #include "../../include/moe_mi355x.h"
 #include "expert_gemm.h"
+#include "decode.h"
 
 namespace moe {
 hipError_t launch_route(const uint16_t* logits, long long ld, int T, int E, int k, long long* idx64,
@@ -73,6 +74,12 @@ int hip_check(hipError_t e, const char* what) {
     int rc_ = hip_check((expr), what);          \
     if (rc_ != MOE_OK) return rc_;              \
   } while (0)
+
+// The three-launch decode path (decode.hip) for T <= 4 unless MOE_DECODE=0.
+bool decode_enabled() {
+  const char* env = getenv("MOE_DECODE");
+  return !(env && env[0] == '0');
+}
 
 size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
 
@@ -422,6 +429,7 @@ ExpertsWs carve_experts(void* base, int T, int H, int E, int k, int I, bool fp8)
   w.bm = tile_rows_for(T, fp8, H, I, I);
   w.MT = max_tiles_of(T, k, E, w.bm, 0);
   w.sync = c.take<int>(kSyncBytes / sizeof(int));
+  w.idx32 = c.take<int>(P);
   w.counts = c.take<int>(E);
   w.offsets = c.take<int>(E);
   w.order = c.take<int>(P);
@@ -459,6 +467,23 @@ int moe_experts_forward(const void* x, int T, int H, int E, int k, int I,
   CHECK_ARG(workspace && workspace_bytes >= w.bytes, "workspace too small: %zu < %zu",
             workspace_bytes, w.bytes);
   hipStream_t s = (hipStream_t)stream;
+  if (decode_enabled()) {
+    DecodeArgs d{};
+    d.x = static_cast<const uint16_t*>(x);
+    d.T = T, d.H = H, d.E = E, d.k = k, d.I = I;
+    d.gate_up = gate_up, d.gu_scale = gu_scale, d.down = down, d.dn_scale = dn_scale;
+    d.fp8 = wdtype == MOE_WEIGHTS_FP8_E4M3;
+    d.round_w = mode == MOE_ROUND_PRODUCT;
+    d.ids_in = top_k_index;
+    d.idx32 = w.idx32;
+    d.wts = const_cast<uint16_t*>(static_cast<const uint16_t*>(top_k_weights));
+    d.act = w.act;
+    d.out = static_cast<uint16_t*>(out);
+    if (decode_fits(d)) {
+      HIP_TRY(launch_decode_gate_up(d, s), "decode gate_up launch");
+      return hip_check(launch_decode_down(d, s), "decode down launch");
+    }
+  }
   HIP_TRY(launch_route_sort(nullptr, 0, nullptr, top_k_index, T, E, k, w.bm, 0, nullptr, nullptr,
                             nullptr, w.counts, w.offsets, w.order, w.table, w.MT, w.scratch, s),
           "sort launch");
@@ -552,6 +577,32 @@ int moe_block_forward(const void* x, int T, int H, int E, int k, int I, int IS,
   uint16_t* lg = logits ? static_cast<uint16_t*>(logits) : w.logits;
   long long* i64 = top_k_index ? top_k_index : w.idx64;
   uint16_t* wt = top_k_weights ? static_cast<uint16_t*>(top_k_weights) : w.w;
+  if (decode_enabled()) {
+    DecodeArgs d{};
+    d.x = static_cast<const uint16_t*>(x);
+    d.T = T, d.H = H, d.E = E, d.k = k, d.I = I, d.IS = IS;
+    d.w_pack = static_cast<const uint16_t*>(w_pack);
+    d.n_pack = n_pack;
+    d.gate_up = gate_up, d.gu_scale = gu_scale, d.down = down, d.dn_scale = dn_scale;
+    d.fp8 = wdtype == MOE_WEIGHTS_FP8_E4M3;
+    d.sh_gate = static_cast<const uint16_t*>(sh_gate);
+    d.sh_up = static_cast<const uint16_t*>(sh_up);
+    d.sh_down = static_cast<const uint16_t*>(sh_down);
+    d.residual = static_cast<const uint16_t*>(residual);
+    d.round_w = mode == MOE_ROUND_PRODUCT;
+    d.logits = lg;
+    d.idx64 = i64;
+    d.idx32 = w.idx32;
+    d.wts = wt;
+    d.act = w.act;
+    d.act_sh = w.act_sh;
+    d.out = static_cast<uint16_t*>(out);
+    if (decode_fits(d)) {
+      HIP_TRY(launch_decode_router(d, s), "decode router launch");
+      HIP_TRY(launch_decode_gate_up(d, s), "decode gate_up launch");
+      return hip_check(launch_decode_down(d, s), "decode down launch");
+    }
+  }
   bool routed_in_router = false;
   if (fuse_enabled("route") && sort_uses_small(T * k, E)) {
     FuseArgs fa{};

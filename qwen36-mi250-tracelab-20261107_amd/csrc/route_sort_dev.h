@@ -88,10 +88,15 @@ __device__ void route_row(const uint16_t* __restrict__ lrow, int E, int k, int l
                           int& my_idx, float& my_w) {
   float p[EPL];
   float m = -INFINITY;
+  // all EPL loads in flight at once (clamped addresses, masked after): one memory round
+  // trip, not one per element
+  uint16_t raw[EPL];
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) raw[i] = lrow[min(lane + kWave * i, E - 1)];
 #pragma unroll
   for (int i = 0; i < EPL; ++i) {
     int e = lane + kWave * i;
-    float z = e < E ? bf_bits2f(lrow[e]) : -INFINITY;
+    float z = e < E ? bf_bits2f(raw[i]) : -INFINITY;
     p[i] = z;
     m = fmaxf(m, z);
   }
