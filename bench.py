@@ -11,8 +11,8 @@ replayed; K is rounded up to a multiple of L and the JSON reports the K timed.
 The headline workload is C2 (decode batch 1, H2048 E256 top-8 + shared, I=IS=512, bf16):
 ``value`` = microseconds per layer (lower is better). The same line carries the C3
 (batch 64, Zipf(1.1) routing), C4 (4096-token prefill) and C5 (40-layer fp8 stack at
-batch 32) results, the roofline of the dominant kernel (the grouped gate_up launch, timed
-with HIP events on the stream it runs on) and the CPU baseline (the CPU torch oracle of
+batch 32) results, the roofline of the dominant kernel (the gate_up launch the block uses
+for that batch size, timed with HIP events on the stream it runs on) and the CPU baseline (the CPU torch oracle of
 the reference path, timed on this host's cores on a bounded sample).
 """
 
@@ -55,10 +55,8 @@ def make_layer(torch, dev, seed, zipf=False, fp8=False):
     router = rnd(E, H)
     v = None
     if zipf:
-        from oracle import moe_oracle as orc  # noqa: PLC0415 - synthetic-input construction only
-
-        r, v = orc.zipf_router(router.cpu(), seed=seed)
-        v = v * orc.ZIPF_MU
+        r, v = load_pkg().synth.zipf_router(router.cpu(), seed=seed)
+        v = v * load_pkg().synth.ZIPF_MU
         router = r.to(dev)
         v = v.to(dev)
     gu, dn = rnd(E, 2 * I, H), rnd(E, H, I)
@@ -102,10 +100,16 @@ def layer_bytes(D, T, fp8=False):
     return weights + acts
 
 
-def gate_up_bytes(D, T, fp8=False):
-    """Algorithmic bytes of the grouped gate_up launch (routed + shared)."""
+def gate_up_bytes(D, T, fp8=False, shared=True):
+    """Algorithmic bytes of one gate_up launch: each distinct expert's gate/up rows once
+    (+ fp32 row scales), the token rows, the activations written; with ``shared`` the
+    shared expert's rows and activations (grouped launch), without it the router logits
+    the decode launch routes from."""
     per_expert = 2 * I * H * (1 if fp8 else 2) + (2 * I * 4 if fp8 else 0)
-    return D * per_expert + 2 * IS * H * 2 + T * H * 2 + (T * K_TOP * I + T * IS) * 2
+    b = D * per_expert + T * H * 2 + T * K_TOP * I * 2
+    if shared:
+        return b + 2 * IS * H * 2 + T * IS * 2
+    return b + T * 320 * 2  # logits rows [T, n_pack = 320]
 
 
 def capture(torch, fn):
@@ -187,26 +191,38 @@ def run_config(torch, dev, name, T, layers, steps, warmup, zipf=False, fp8=False
         res["mfma_frac_bf16"] = round(flops / (us_layer * 1e-6) / 1e12 / BF16_PEAK_TFLOPS, 4)
     del graph
 
-    # the dominant kernel alone: the grouped gate_up launch of each layer (routed + shared)
+    # the dominant kernel alone, as the block launches it: the decode gate_up (routing in the
+    # launch, routed experts) for decode-path shapes, else the grouped gate_up (routed +
+    # shared) over the sorted tile table
+    decode = pkg.ops.decode_fits(T, H, E, K_TOP, I, IS)
     sps = []
     for mlp, x in zip(mlps, xs):
         logits = pkg.ops.router_logits(x, pkg.block.pack_router(mlp))
-        _, idx, _ = pkg.ops.route(logits, K_TOP, experts=E)
-        sps.append(pkg.ops.sort_pairs(idx, E, shared=True))
+        if decode:
+            sps.append(logits)
+        else:
+            _, idx, _ = pkg.ops.route(logits, K_TOP, experts=E)
+            sps.append(pkg.ops.sort_pairs(idx, E, shared=True))
     torch.cuda.synchronize()
 
     def gate_up_pass():
         for mlp, x, sp in zip(mlps, xs, sps):
             ex = mlp.experts
-            pkg.ops.grouped_gate_up(x, K_TOP, ex.gate_up_proj, sp,
-                                    scale=getattr(ex, "gate_up_scale", None),
-                                    shared=(mlp.shared_expert.gate_proj.weight,
-                                            mlp.shared_expert.up_proj.weight))
+            scale = getattr(ex, "gate_up_scale", None)
+            if decode:
+                pkg.ops.decode_gate_up(x, ex.gate_up_proj, K_TOP, logits=sp, experts=E,
+                                       scale=scale)
+            else:
+                pkg.ops.grouped_gate_up(x, K_TOP, ex.gate_up_proj, sp, scale=scale,
+                                        shared=(mlp.shared_expert.gate_proj.weight,
+                                                mlp.shared_expert.up_proj.weight))
 
     graph = capture(torch, gate_up_pass)
     ms = time_graph(torch, graph, reps, wreps)
     us_k = ms * 1000.0 / nsteps
-    kbytes = sum(gate_up_bytes(d, T, fp8) for d in Ds) / len(Ds)
+    kbytes = sum(gate_up_bytes(d, T, fp8, shared=not decode) for d in Ds) / len(Ds)
+    res["gate_up_kernel"] = "k_dec_gate_up" if decode else (
+        "k_prefill_gemm" if T > 512 and not fp8 else "k_expert_gemm")
     res["gate_up_us"] = round(us_k, 3)
     res["gate_up_bytes"] = int(kbytes)
     res["gate_up_GBps"] = round(kbytes / (us_k * 1e-6) / 1e9, 1)
@@ -302,7 +318,7 @@ def main():
         "hbm_TBps": head["layer_TBps"],
         "hbm_frac": head["layer_hbm_frac"],
         "tokens_per_s": head["tokens_per_s"],
-        "roofline": {"bound": "hbm", "kernel": "grouped gate_up (k_expert_gemm SWIGLU)",
+        "roofline": {"bound": "hbm", "kernel": head["gate_up_kernel"],
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
                      "bytes_per_launch": kbytes, "us_per_launch": kus},

@@ -118,6 +118,39 @@ int moe_combine(const void* y, const void* w, int T, int H, int k, const void* y
                 const void* seg, long long ld_seg, const void* residual, void* out, int mode,
                 void* stream);
 
+/* Decode stages (T <= 4 tokens; H a multiple of 512 up to 4096, I and IS 512 or 1024,
+ * E <= 512, T*k <= 64): the three launches of engine/fast/fused.py's FusedDecode._moe
+ * (fused.py:887-932). moe_decode_fits says whether a shape takes this path; the fused
+ * entry points below use it on their own for such shapes (MOE_DECODE=0 turns it off). */
+int moe_decode_fits(int T, int H, int E, int k, int I, int IS);
+
+/* Stage 1: router logits [T, n_pack] (as moe_router_logits) and, with sh_gate / sh_up
+ * [IS, H], act_sh [T, IS] = bf16(bf16(silu(bf16 g)) * bf16 u) of the shared expert in the
+ * same launch. Replaces the packed router|shared GEMV of fused.py:745-746 / 798-840. */
+int moe_decode_router(const void* x, int T, int H, const void* w_pack, int n_pack,
+                      const void* sh_gate, const void* sh_up, int IS, void* logits, void* act_sh,
+                      void* stream);
+
+/* Stage 2: act [T*k, I] = SwiGLU of the routed experts. With logits (first E columns, row
+ * stride n_pack) the softmax / top-k runs inside the launch and the routing is written to
+ * idx32 [T, k], top_k_weights [T, k] bf16 and idx64 [T, k] (optional); without, idx64_in
+ * gives it and idx32 receives a copy. Replaces _topk (fused.py:554-570) and
+ * _moe_up_kernel with FUSE_TOPK (fused.py:582-632). */
+int moe_decode_gate_up(const void* x, int T, int H, int E, int k, int I, const void* logits,
+                       int n_pack, const long long* idx64_in, const void* gate_up,
+                       const float* gu_scale, int wdtype, int* idx32, void* top_k_weights,
+                       long long* idx64, void* act, void* stream);
+
+/* Stage 3: out [T, H] = bf16(bf16(sum_j term_j) + bf16(bf16(sigmoid(seg)) * y_sh))
+ * (+ residual), term_j = bf16(w_j * bf16(act_p . Wd[e_p])) under MOE_ROUND_PRODUCT, with
+ * y_sh = bf16(act_sh . Wsd) and seg = logits[t, E]. sh_down null: routed experts only (no
+ * shared term; logits unused). Replaces _moe_down_kernel (fused.py:635-692). */
+int moe_decode_down(const void* act, int T, int H, int E, int k, int I, const int* idx32,
+                    const void* top_k_weights, const void* down, const float* dn_scale,
+                    int wdtype, const void* sh_down, int IS, const void* act_sh,
+                    const void* logits, int n_pack, const void* residual, int mode, void* out,
+                    void* stream);
+
 /* Routed experts only (surface 1): the experts_forward(self, hidden_states, top_k_index,
  * top_k_weights) of engine/experts.py:93-102 (batched_mm for T <= 16, padded bmm above).
  * out [T, H] bf16. */

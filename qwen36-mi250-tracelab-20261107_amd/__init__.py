@@ -12,7 +12,7 @@ include/moe_mi355x.h):
 - ``fp8``: per-row fp8-e4m3 expert weights.
 """
 
-from . import _lib, block, experts, fp8, ops  # noqa: F401
+from . import _lib, block, experts, fp8, ops, synth  # noqa: F401
 from ._lib import MoeLibraryError  # noqa: F401
 from .block import moe, pack_router  # noqa: F401
 from .experts import NAME, experts_forward, register  # noqa: F401

@@ -412,6 +412,94 @@ int moe_combine(const void* y, const void* w, int T, int H, int k, const void* y
                    "combine launch");
 }
 
+// ------------------------------------------------------------------------ decode stages
+
+int moe_decode_fits(int T, int H, int E, int k, int I, int IS) {
+  DecodeArgs d{};
+  d.T = T, d.H = H, d.E = E, d.k = k, d.I = I, d.IS = IS;
+  d.logits = reinterpret_cast<uint16_t*>(16);  // routing inside the launch
+  d.sh_down = IS > 0 ? reinterpret_cast<const uint16_t*>(16) : nullptr;
+  return decode_fits(d) ? 1 : 0;
+}
+
+int moe_decode_router(const void* x, int T, int H, const void* w_pack, int n_pack,
+                      const void* sh_gate, const void* sh_up, int IS, void* logits, void* act_sh,
+                      void* stream) {
+  CHECK_ARG(x && w_pack && logits, "null pointer");
+  CHECK_ARG(!sh_gate || (sh_up && act_sh), "shared gate without shared up / act_sh");
+  CHECK_ARG(T >= 1 && T <= kDecMaxTokens && H % 512 == 0 && H <= 4096 && n_pack >= 1,
+            "decode router shape (T=%d H=%d n_pack=%d) not supported", T, H, n_pack);
+  CHECK_ARG(!sh_gate || (IS >= 1), "bad shared intermediate %d", IS);
+  DecodeArgs d{};
+  d.x = static_cast<const uint16_t*>(x);
+  d.T = T, d.H = H, d.IS = IS;
+  d.w_pack = static_cast<const uint16_t*>(w_pack);
+  d.n_pack = n_pack;
+  d.sh_gate = static_cast<const uint16_t*>(sh_gate);
+  d.sh_up = static_cast<const uint16_t*>(sh_up);
+  d.logits = static_cast<uint16_t*>(logits);
+  d.act_sh = static_cast<uint16_t*>(act_sh);
+  return hip_check(launch_decode_router(d, (hipStream_t)stream), "decode router launch");
+}
+
+int moe_decode_gate_up(const void* x, int T, int H, int E, int k, int I, const void* logits,
+                       int n_pack, const long long* idx64_in, const void* gate_up,
+                       const float* gu_scale, int wdtype, int* idx32, void* top_k_weights,
+                       long long* idx64, void* act, void* stream) {
+  CHECK_ARG(x && gate_up && idx32 && act, "null pointer");
+  CHECK_ARG(logits || idx64_in, "need logits or a given routing");
+  CHECK_ARG(!logits || (top_k_weights && n_pack >= E), "routing outputs / n_pack");
+  CHECK_ARG(wdtype == MOE_WEIGHTS_BF16 || (wdtype == MOE_WEIGHTS_FP8_E4M3 && gu_scale),
+            "bad weight dtype / missing scales");
+  DecodeArgs d{};
+  d.x = static_cast<const uint16_t*>(x);
+  d.T = T, d.H = H, d.E = E, d.k = k, d.I = I;
+  d.gate_up = gate_up, d.gu_scale = gu_scale;
+  d.fp8 = wdtype == MOE_WEIGHTS_FP8_E4M3;
+  d.logits = const_cast<uint16_t*>(static_cast<const uint16_t*>(logits));
+  d.n_pack = n_pack;
+  d.ids_in = idx64_in;
+  d.idx32 = idx32;
+  d.wts = static_cast<uint16_t*>(top_k_weights);
+  d.idx64 = idx64;
+  d.act = static_cast<uint16_t*>(act);
+  CHECK_ARG(decode_fits(d), "decode gate_up shape (T=%d H=%d E=%d k=%d I=%d) not supported", T,
+            H, E, k, I);
+  return hip_check(launch_decode_gate_up(d, (hipStream_t)stream), "decode gate_up launch");
+}
+
+int moe_decode_down(const void* act, int T, int H, int E, int k, int I, const int* idx32,
+                    const void* top_k_weights, const void* down, const float* dn_scale,
+                    int wdtype, const void* sh_down, int IS, const void* act_sh,
+                    const void* logits, int n_pack, const void* residual, int mode, void* out,
+                    void* stream) {
+  CHECK_ARG(act && idx32 && top_k_weights && down && out, "null pointer");
+  CHECK_ARG(!sh_down || (act_sh && logits && n_pack > E), "shared expert needs act_sh, logits");
+  CHECK_ARG(mode == MOE_ROUND_PRODUCT || mode == MOE_EXACT_PRODUCT, "bad mode %d", mode);
+  CHECK_ARG(wdtype == MOE_WEIGHTS_BF16 || (wdtype == MOE_WEIGHTS_FP8_E4M3 && dn_scale),
+            "bad weight dtype / missing scales");
+  DecodeArgs d{};
+  d.T = T, d.H = H, d.E = E, d.k = k, d.I = I, d.IS = IS;
+  d.down = down, d.dn_scale = dn_scale;
+  d.fp8 = wdtype == MOE_WEIGHTS_FP8_E4M3;
+  d.sh_down = static_cast<const uint16_t*>(sh_down);
+  d.act_sh = const_cast<uint16_t*>(static_cast<const uint16_t*>(act_sh));
+  d.logits = const_cast<uint16_t*>(static_cast<const uint16_t*>(logits));
+  d.n_pack = n_pack;
+  d.residual = static_cast<const uint16_t*>(residual);
+  d.round_w = mode == MOE_ROUND_PRODUCT;
+  d.idx32 = const_cast<int*>(idx32);
+  d.wts = const_cast<uint16_t*>(static_cast<const uint16_t*>(top_k_weights));
+  d.act = const_cast<uint16_t*>(static_cast<const uint16_t*>(act));
+  d.out = static_cast<uint16_t*>(out);
+  const uint16_t* lg = d.logits;
+  d.logits = nullptr;  // the E bound of the in-launch routing does not apply here
+  CHECK_ARG(decode_fits(d), "decode down shape (T=%d H=%d k=%d I=%d IS=%d) not supported", T, H,
+            k, I, IS);
+  d.logits = const_cast<uint16_t*>(lg);
+  return hip_check(launch_decode_down(d, (hipStream_t)stream), "decode down launch");
+}
+
 // ------------------------------------------------------------------ routed experts only
 
 namespace {

@@ -13,6 +13,9 @@ caching allocator; weights are read in place. Nothing here synchronises with the
   combine            weighted sum + gated shared expert (engine/fast/prefill_kernels.py:253-273)
   moe_decode         routed experts, batched_mm rounding (engine/fast/kernels.py:171-217)
   moe_prefill        routed experts, fp32 weighting      (engine/fast/moe_prefill.py:546-582)
+  decode_router      router | shared gate_up, T <= 4    (engine/fast/fused.py:745-746, 798-840)
+  decode_gate_up     top-k + routed gate_up, T <= 4      (engine/fast/fused.py:554-632)
+  decode_down        down + combine + shared, T <= 4     (engine/fast/fused.py:635-692)
 """
 
 from __future__ import annotations
@@ -279,3 +282,97 @@ def moe_prefill(x, top_k_index, top_k_weights, gate_up, down, **scales) -> torch
     """Routed experts with the grouped / padded rounding (engine/fast/moe_prefill.py:546):
     w * y exact in fp32, summed in fp32, rounded once."""
     return experts(x, top_k_index, top_k_weights, gate_up, down, round_products=False, **scales)
+
+
+# ----------------------------------------------------------------- decode stages (T <= 4)
+
+
+def decode_fits(tokens: int, hidden: int, experts: int, top_k: int, inter: int,
+                inter_shared: int = 0) -> bool:
+    """Whether a shape takes the three-launch decode path."""
+    return bool(_lib.load().moe_decode_fits(tokens, hidden, experts, top_k, inter, inter_shared))
+
+
+def decode_router(x: torch.Tensor, w_pack: torch.Tensor, shared: tuple | None = None):
+    """(logits [T, n_pack], act_sh [T, IS] or None): the router rows and, with
+    ``shared=(sh_gate, sh_up)``, the shared expert's SwiGLU in the same launch."""
+    _need_cuda(x, w_pack)
+    x = _bf16(x, "x")
+    w_pack = _bf16(w_pack, "w_pack")
+    tokens, hidden = x.shape
+    n_pack = w_pack.shape[0]
+    logits = torch.empty((tokens, n_pack), dtype=torch.bfloat16, device=x.device)
+    sg = su = act_sh = None
+    inter_s = 0
+    if shared is not None:
+        sg, su = (_bf16(w, "shared weight") for w in shared)
+        inter_s = sg.shape[0]
+        act_sh = torch.empty((tokens, inter_s), dtype=torch.bfloat16, device=x.device)
+    check(_lib.load().moe_decode_router(ptr(x), tokens, hidden, ptr(w_pack), n_pack, ptr(sg),
+                                        ptr(su), inter_s, ptr(logits), ptr(act_sh),
+                                        stream_of(x)), "decode_router")
+    return logits, act_sh
+
+
+def decode_gate_up(x: torch.Tensor, gate_up: torch.Tensor, top_k: int, *, logits=None,
+                   experts: int | None = None, top_k_index=None, scale=None):
+    """(act [T*k, I], idx32 [T, k], top_k_weights [T, k] bf16 or None, top_k_index int64
+    or None). With ``logits`` the routing (softmax / top-k over the first ``experts``
+    columns) runs inside the launch; else ``top_k_index`` gives it."""
+    _need_cuda(x, gate_up)
+    x = _bf16(x, "x")
+    gu, gus, wd = expert_weight(gate_up, scale, "gate_up")
+    e_all, two_i, hidden = gu.shape
+    experts = e_all if experts is None else experts
+    tokens = x.shape[0]
+    dev = x.device
+    idx32 = torch.empty((tokens, top_k), dtype=torch.int32, device=dev)
+    act = torch.empty((tokens * top_k, two_i // 2), dtype=torch.bfloat16, device=dev)
+    wts = idx64 = idx_in = None
+    n_pack = 0
+    if logits is not None:
+        logits = _bf16(logits, "logits")
+        n_pack = logits.shape[1]
+        wts = torch.empty((tokens, top_k), dtype=torch.bfloat16, device=dev)
+        idx64 = torch.empty((tokens, top_k), dtype=torch.long, device=dev)
+    else:
+        if top_k_index is None:
+            raise ValueError("decode_gate_up needs logits or top_k_index")
+        idx_in = top_k_index.to(torch.long).contiguous()
+    check(_lib.load().moe_decode_gate_up(ptr(x), tokens, hidden, experts, top_k, two_i // 2,
+                                         ptr(logits), n_pack, ptr(idx_in), ptr(gu), ptr(gus), wd,
+                                         ptr(idx32), ptr(wts), ptr(idx64), ptr(act),
+                                         stream_of(x)), "decode_gate_up")
+    return act, idx32, wts, idx64
+
+
+def decode_down(act: torch.Tensor, tokens: int, top_k: int, down: torch.Tensor,
+                idx32: torch.Tensor, top_k_weights: torch.Tensor, *, round_products: bool = True,
+                scale=None, shared: tuple | None = None, logits=None, experts: int | None = None,
+                residual=None) -> torch.Tensor:
+    """out [T, H]: the routed down projections combined in routing order, plus (with
+    ``shared=(sh_down, act_sh)`` and the logits holding the shared-gate logit at column
+    ``experts``) the gated shared expert, plus ``residual``."""
+    _need_cuda(act, down, idx32, top_k_weights)
+    act = _bf16(act, "act")
+    dn, dns, wd = expert_weight(down, scale, "down")
+    e_all, hidden, inter = dn.shape
+    experts = e_all if experts is None else experts
+    wts = _bf16(top_k_weights, "top_k_weights")
+    idx32 = idx32.to(torch.int32).contiguous()
+    sd = act_sh = None
+    inter_s = n_pack = 0
+    if shared is not None:
+        sd, act_sh = (_bf16(t, "shared") for t in shared)
+        inter_s = sd.shape[1]
+        logits = _bf16(logits, "logits")
+        n_pack = logits.shape[1]
+    if residual is not None:
+        residual = _bf16(residual, "residual")
+    out = torch.empty((tokens, hidden), dtype=torch.bfloat16, device=act.device)
+    mode = _lib.ROUND_PRODUCT if round_products else _lib.EXACT_PRODUCT
+    check(_lib.load().moe_decode_down(ptr(act), tokens, hidden, experts, top_k, inter, ptr(idx32),
+                                      ptr(wts), ptr(dn), ptr(dns), wd, ptr(sd), inter_s,
+                                      ptr(act_sh), ptr(logits), n_pack, ptr(residual), mode,
+                                      ptr(out), stream_of(act)), "decode_down")
+    return out

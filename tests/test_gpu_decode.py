@@ -155,3 +155,23 @@ def test_decode_fp8_block(pkg, dev, layer, T):
     assert max_abs(out, f32_q) <= 2e-2 and mean_rel(out, f32_q) <= 6e-3
     if torch.equal(idx, t_idx):
         assert max_abs(out, t_out) <= 4e-3
+
+
+def test_decode_stages_compose_to_block(pkg, dev, layer):
+    """The operator-level stages (decode_router -> decode_gate_up -> decode_down) give the
+    block's bits."""
+    mlp = _mlp(layer, dev)
+    x = torch.randn(2, 2048, generator=torch.Generator().manual_seed(3)).to(BF16).to(dev)
+    pack = pkg.block.pack_router(mlp)
+    sh = mlp.shared_expert
+    logits, act_sh = pkg.ops.decode_router(x, pack, shared=(sh.gate_proj.weight, sh.up_proj.weight))
+    act, idx32, wts, idx64 = pkg.ops.decode_gate_up(x, layer["gate_up"], 8, logits=logits,
+                                                    experts=256)
+    out = pkg.ops.decode_down(act, 2, 8, layer["down"], idx32, wts,
+                              shared=(sh.down_proj.weight, act_sh), logits=logits, experts=256)
+    b_out, b_idx, b_wts, b_lg = pkg.block.moe(x, mlp, 8, decode=True, return_routing=True)
+    torch.cuda.synchronize()
+    assert torch.equal(logits, b_lg)
+    assert torch.equal(idx64, b_idx) and torch.equal(idx32.long(), b_idx)
+    assert torch.equal(wts, b_wts)
+    assert torch.equal(out, b_out)

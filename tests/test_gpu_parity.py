@@ -19,6 +19,12 @@ pytestmark = pytest.mark.gpu
 TOL = 2e-2
 
 
+def _synth():
+    import __graft_entry__
+
+    return __graft_entry__.load_package().synth
+
+
 def _say(*a):
     print(*a, flush=True)
 
@@ -224,7 +230,7 @@ def _full_weights(dev, seed=0, zipf=False):
     }
     v = None
     if zipf:
-        r, v = orc.zipf_router(w["router"].cpu(), seed=seed)
+        r, v = _synth().zipf_router(w["router"].cpu(), seed=seed)
         w["router"] = r.to(dev)
     return w, v
 

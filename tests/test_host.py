@@ -83,3 +83,20 @@ def test_fp8_quantize_matches_oracle(pkg):
     q2, s2 = orc.quantize_rows(w)
     assert torch.equal(q.view(torch.uint8), q2.view(torch.uint8)) and torch.equal(s, s2)
     assert q.dtype == torch.float8_e4m3fn and s.shape == (3, 32)
+
+
+def test_decode_fits_predicate(pkg):
+    """The decode path's shape limits: T <= 4, T*k <= 64, H a multiple of 512 up to 4096,
+    I and IS in {512, 1024}, E <= 512 (routing inside the launch)."""
+    fits = pkg.ops.decode_fits
+    assert fits(1, 2048, 256, 8, 512, 512)
+    assert fits(4, 2048, 256, 8, 512, 512)
+    assert fits(4, 4096, 512, 16, 1024, 1024)
+    assert not fits(5, 2048, 256, 8, 512, 512)
+    assert not fits(0, 2048, 256, 8, 512, 512)
+    assert not fits(1, 2048 + 256, 256, 8, 512, 512)
+    assert not fits(1, 8192, 256, 8, 512, 512)
+    assert not fits(1, 2048, 256, 8, 256, 512)
+    assert not fits(1, 2048, 256, 8, 512, 768)
+    assert not fits(1, 2048, 1024, 8, 512, 512)
+    assert not fits(4, 2048, 256, 17, 512, 512)

@@ -23,6 +23,12 @@ def test_route_matches_bruteforce_on_tied_rows(E, k):
     assert torch.equal(idx, orc.route_bruteforce(logits, k))
 
 
+def _synth():
+    import __graft_entry__
+
+    return __graft_entry__.load_package().synth
+
+
 def test_route_tie_rule_is_lowest_index():
     logits = torch.zeros(1, 16, dtype=BF16)
     logits[0, [3, 7, 10, 12]] = 1.0
@@ -271,8 +277,8 @@ def test_zipf_router_distinct_experts():
     router = (torch.randn(256, 2048, generator=g) * 0.02).to(BF16)
     ds = []
     for seed in range(3):
-        w, v = orc.zipf_router(router, seed=seed)
-        x = (torch.randn(64, 2048, generator=g) + orc.ZIPF_MU * v).to(BF16)
+        w, v = _synth().zipf_router(router, seed=seed)
+        x = (torch.randn(64, 2048, generator=g) + _synth().ZIPF_MU * v).to(BF16)
         _, idx = orc.route(F.linear(x, w), 8)
         ds.append(int(torch.unique(idx).numel()))
     assert all(115 <= d <= 165 for d in ds), ds
