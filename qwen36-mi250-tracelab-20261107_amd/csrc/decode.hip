@@ -62,10 +62,10 @@ template <bool FP8>
 __device__ __forceinline__ WFrag<FP8> ldraw(const void* row, int elem) {
   WFrag<FP8> f;
   if (FP8) {
-    uint2 q = *reinterpret_cast<const uint2*>(static_cast<const uint8_t*>(row) + elem);
+    uint2 q = ld8_stream(static_cast<const uint8_t*>(row) + elem);
     f.v = make_uint4(q.x, q.y, 0u, 0u);
   } else {
-    f.v = ld16(static_cast<const uint16_t*>(row) + elem);
+    f.v = ld16_stream(static_cast<const uint16_t*>(row) + elem);
   }
   return f;
 }
@@ -98,10 +98,10 @@ __global__ __launch_bounds__(64) void k_dec_router(DecodeArgs a) {
   const uint16_t* r1 = router ? r0 : a.sh_up + (long long)n * H;
   uint4 w0[HC], w1[HC];
 #pragma unroll
-  for (int c = 0; c < HC; ++c) w0[c] = ld16(r0 + c * 512 + lane * 8);
+  for (int c = 0; c < HC; ++c) w0[c] = ld16_stream(r0 + c * 512 + lane * 8);
   if (!router) {
 #pragma unroll
-    for (int c = 0; c < HC; ++c) w1[c] = ld16(r1 + c * 512 + lane * 8);
+    for (int c = 0; c < HC; ++c) w1[c] = ld16_stream(r1 + c * 512 + lane * 8);
   }
   uint4 xv[NT][HC];
 #pragma unroll
@@ -156,36 +156,55 @@ __global__ __launch_bounds__(kDecThreads) void k_dec_gate_up(DecodeArgs a) {
     for (int c = 0; c < HC; ++c)
       xv[t][c] = ld16(a.x + (long long)min(t, a.T - 1) * H + c * 512 + lane * 8);
 
-  if (a.logits) {
-    if (wave < a.T) {
-      int my_idx;
-      float my_w;
-      route_row<EPL>(a.logits + (long long)wave * a.n_pack, a.E, a.k, lane, my_idx, my_w);
-      if (lane < a.k) {
-        const int p = wave * a.k + lane;
-        const uint16_t wb = f2bf_bits(my_w);
-        s_idx[p] = my_idx;
-        if (blockIdx.x == 0) {
-          a.idx32[p] = my_idx;
-          a.wts[p] = wb;
-          if (a.idx64) a.idx64[p] = my_idx;
+  // key: the expert of pair `lane` (lanes < P); distinct: the pairs' experts are known to
+  // differ (one token routed here)
+  int key = 0;
+  bool distinct = false;
+  if (NT == 1 && a.logits) {
+    // one token: every wave routes it itself (no LDS round trip, no barrier)
+    int my_idx;
+    float my_w;
+    route_row<EPL>(a.logits, a.E, a.k, lane, my_idx, my_w);
+    key = my_idx;
+    distinct = true;
+    if (blockIdx.x == 0 && wave == 0 && lane < a.k) {
+      a.idx32[lane] = my_idx;
+      a.wts[lane] = f2bf_bits(my_w);
+      if (a.idx64) a.idx64[lane] = my_idx;
+    }
+  } else {
+    if (a.logits) {
+      if (wave < a.T) {
+        int my_idx;
+        float my_w;
+        route_row<EPL>(a.logits + (long long)wave * a.n_pack, a.E, a.k, lane, my_idx, my_w);
+        if (lane < a.k) {
+          const int p = wave * a.k + lane;
+          s_idx[p] = my_idx;
+          if (blockIdx.x == 0) {
+            a.idx32[p] = my_idx;
+            a.wts[p] = f2bf_bits(my_w);
+            if (a.idx64) a.idx64[p] = my_idx;
+          }
         }
       }
+    } else if (threadIdx.x < P) {
+      const long long v = a.ids_in[threadIdx.x];
+      const int e = (int)(v < 0 ? 0 : (v >= a.E ? a.E - 1 : v));
+      s_idx[threadIdx.x] = e;
+      if (blockIdx.x == 0) a.idx32[threadIdx.x] = e;
     }
-  } else if (threadIdx.x < P) {
-    const long long v = a.ids_in[threadIdx.x];
-    const int e = (int)(v < 0 ? 0 : (v >= a.E ? a.E - 1 : v));
-    s_idx[threadIdx.x] = e;
-    if (blockIdx.x == 0) a.idx32[threadIdx.x] = e;
+    __syncthreads();
+    key = lane < P ? s_idx[lane] : -1;
   }
-  __syncthreads();
 
   // distinct experts numbered in first-use order (pair order)
-  const int key = lane < P ? s_idx[lane] : -1;
   bool first = lane < P;
-  for (int q = 0; q < P; ++q) {
-    const int kq = s_idx[q];
-    if (q < lane && kq == key) first = false;
+  if (!distinct) {
+    for (int q = 0; q < P; ++q) {
+      const int kq = __builtin_amdgcn_readlane(key, q);
+      if (q < lane && kq == key) first = false;
+    }
   }
   const unsigned long long fmask = __ballot(first);
   const int rank = __popcll(fmask & ((1ull << lane) - 1ull));
@@ -260,7 +279,7 @@ __global__ __launch_bounds__(kDecThreads) void k_dec_down(DecodeArgs a) {
   if (shared) {
 #pragma unroll
     for (int c = 0; c < 2; ++c)
-      if (c < isc) ws[c] = ld16(a.sh_down + (long long)n * a.IS + c * 512 + lane * 8);
+      if (c < isc) ws[c] = ld16_stream(a.sh_down + (long long)n * a.IS + c * 512 + lane * 8);
 #pragma unroll
     for (int t = 0; t < NT; ++t)
 #pragma unroll

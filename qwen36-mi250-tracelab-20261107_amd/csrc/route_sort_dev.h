@@ -49,92 +49,191 @@ __device__ __forceinline__ float wave_sum(float v) {
   return (rowlane(v, 0) + rowlane(v, 16)) + (rowlane(v, 32) + rowlane(v, 48));
 }
 
-// (p, expert) pair order of the routing: larger p first, the lower expert on ties.
-__device__ __forceinline__ bool better(float pa, int ia, float pb, int ib) {
-  return pa > pb || (pa == pb && ia < ib);
+constexpr int kDppBcast15 = 0x142;  // row_bcast:15 (rows 1, 3 <- last lane of the row before)
+constexpr int kDppBcast31 = 0x143;  // row_bcast:31 (rows 2, 3 <- lane 31)
+
+template <int CTRL, int ROWS = 0xF>
+__device__ __forceinline__ uint32_t max_dpp_u32(uint32_t v) {
+  // lanes outside ROWS (and invalid sources) read 0, the identity of the max
+  const uint32_t o = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROWS, 0xF, true);
+  return o > v ? o : v;
 }
-template <int CTRL>
-__device__ __forceinline__ void argmax_dpp(float& v, int& i) {
-  float ov = dppf<CTRL>(v);
-  int oi = dppi<CTRL>(i);
-  if (better(ov, oi, v, i)) {
-    v = ov;
-    i = oi;
-  }
+template <int CTRL, int ROWS = 0xF>
+__device__ __forceinline__ int min_dpp_i32(int v) {
+  const int o = __builtin_amdgcn_update_dpp(0x7fffffff, v, CTRL, ROWS, 0xF, false);
+  return o < v ? o : v;
 }
-// Wave-uniform argmax of (v, i) under ``better``.
-__device__ __forceinline__ void wave_argmax(float& v, int& i) {
-  argmax_dpp<kDppXor1>(v, i);
-  argmax_dpp<kDppXor2>(v, i);
-  argmax_dpp<kDppHalfMirror>(v, i);
-  argmax_dpp<kDppMirror>(v, i);
-  float bv = rowlane(v, 0);
-  int bi = __builtin_amdgcn_readlane(i, 0);
-#pragma unroll
-  for (int r = 16; r < 64; r += 16) {
-    float ov = rowlane(v, r);
-    int oi = __builtin_amdgcn_readlane(i, r);
-    if (better(ov, oi, bv, bi)) {
-      bv = ov;
-      bi = oi;
-    }
-  }
-  v = bv;
-  i = bi;
+// Wave-uniform max / min: DPP within rows, row broadcasts across them (lane 63 ends with
+// the result), one readlane. No branches, no LDS.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = max_dpp_u32<kDppXor1>(v);
+  v = max_dpp_u32<kDppXor2>(v);
+  v = max_dpp_u32<kDppHalfMirror>(v);
+  v = max_dpp_u32<kDppMirror>(v);
+  v = max_dpp_u32<kDppBcast15, 0xA>(v);
+  v = max_dpp_u32<kDppBcast31, 0xC>(v);
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+__device__ __forceinline__ int wave_min_i32(int v) {
+  v = min_dpp_i32<kDppXor1>(v);
+  v = min_dpp_i32<kDppXor2>(v);
+  v = min_dpp_i32<kDppHalfMirror>(v);
+  v = min_dpp_i32<kDppMirror>(v);
+  v = min_dpp_i32<kDppBcast15, 0xA>(v);
+  v = min_dpp_i32<kDppBcast31, 0xC>(v);
+  return __builtin_amdgcn_readlane(v, 63);
 }
 
+// Routing order of (p, expert) entries: larger p first, the lower expert on equal p. p >= 0,
+// so its fp32 bits order like its values; empty entries carry p bits 0 and expert INT_MAX
+// (below every real entry: equal p bits resolve to the lower expert).
+__device__ __forceinline__ bool route_before(uint32_t pa, int ea, uint32_t pb, int eb) {
+  return pa > pb || (pa == pb && ea < eb);
+}
+__device__ __forceinline__ void cas_desc(uint32_t& pa, int& ea, uint32_t& pb, int& eb) {
+  const bool sw = route_before(pb, eb, pa, ea);
+  const uint32_t tp = pa;
+  const int te = ea;
+  pa = sw ? pb : pa;
+  ea = sw ? eb : ea;
+  pb = sw ? tp : pb;
+  eb = sw ? te : eb;
+}
+
+// Exact selection on the probabilities: each lane's EPL entries sorted in routing order,
+// k rounds take the wave maximum of the lanes' head p and pop the winning head; equal p in
+// several lanes go to the lowest expert through a second reduction.
 template <int EPL>
-__device__ void route_row(const uint16_t* __restrict__ lrow, int E, int k, int lane,
-                          int& my_idx, float& my_w) {
-  float p[EPL];
-  float m = -INFINITY;
-  // all EPL loads in flight at once (clamped addresses, masked after): one memory round
-  // trip, not one per element
-  uint16_t raw[EPL];
-#pragma unroll
-  for (int i = 0; i < EPL; ++i) raw[i] = lrow[min(lane + kWave * i, E - 1)];
+__device__ void route_select_exact(const float* p, int E, int k, int lane, float& mine_p,
+                                   int& mine_i, float& tot) {
+  uint32_t kp[EPL];
+  int ke[EPL];
 #pragma unroll
   for (int i = 0; i < EPL; ++i) {
     int e = lane + kWave * i;
-    float z = e < E ? bf_bits2f(raw[i]) : -INFINITY;
-    p[i] = z;
-    m = fmaxf(m, z);
+    kp[i] = e < E ? __float_as_uint(p[i]) : 0u;
+    ke[i] = e < E ? e : 0x7fffffff;
   }
-  m = wave_max(m);
+#pragma unroll
+  for (int w = 1; w < EPL; ++w)  // insertion network
+#pragma unroll
+    for (int i = w; i > 0; --i) cas_desc(kp[i - 1], ke[i - 1], kp[i], ke[i]);
+  tot = 0.f;
+  for (int j = 0; j < k; ++j) {
+    const uint32_t m = wave_max_u32(kp[0]);
+    bool win = kp[0] == m;
+    const unsigned long long bal = __ballot(win);
+    int e_win;
+    if (__popcll(bal) == 1) {
+      e_win = __builtin_amdgcn_readlane(ke[0], __ffsll((long long)bal) - 1);
+    } else {
+      e_win = wave_min_i32(win ? ke[0] : 0x7fffffff);
+      win = win && ke[0] == e_win;
+    }
+#pragma unroll
+    for (int i = 0; i + 1 < EPL; ++i) {
+      kp[i] = win ? kp[i + 1] : kp[i];
+      ke[i] = win ? ke[i + 1] : ke[i];
+    }
+    if (win) {
+      kp[EPL - 1] = 0u;
+      ke[EPL - 1] = 0x7fffffff;
+    }
+    const float bp = __uint_as_float(m);
+    tot += bp;  // sequential j order
+    if (lane == j) {
+      mine_p = bp;
+      mine_i = e_win;
+    }
+  }
+}
+
+// bf16 logit -> 16-bit key that orders like the value (sign flipped, negatives inverted).
+__device__ __forceinline__ uint32_t bf16_order_key(uint32_t b) {
+  return (b & 0x8000u) ? (~b & 0xffffu) : (b | 0x8000u);
+}
+__device__ __forceinline__ uint32_t bf16_from_order_key(uint32_t k) {
+  return (k & 0x8000u) ? (k & 0x7fffu) : (~k & 0xffffu);
+}
+
+// Softmax / top-k / renormalise of one token's E logits (one wave; lane j < k receives
+// the j-th expert and its weight p_j / sum p_sel). Order: larger p first, the lower expert
+// on equal p (the reference's rule on fp32 p = softmax(bf16 logits)).
+//
+// p is a non-decreasing function of the logit, so the k + 1 largest logits (ties to the
+// lower expert: one 32-bit key per entry) are the k largest p in the same order whenever
+// their p strictly decrease wherever their logits do. That is checked on the selection,
+// and the cases that fail it (p equal for different logits, e.g. exp underflow; a boundary
+// logit under 2^-10 in magnitude or a subnormal boundary p, where fp32 exp need not separate
+// neighbouring logits) take the exact selection on p.
+template <int EPL>
+__device__ void route_row(const uint16_t* __restrict__ lrow, int E, int k, int lane,
+                          int& my_idx, float& my_w) {
+  // all EPL loads in flight at once (clamped addresses, masked after)
+  uint16_t raw[EPL];
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) raw[i] = lrow[min(lane + kWave * i, E - 1)];
+  uint32_t key[EPL];
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) {
+    int e = lane + kWave * i;
+    key[i] = e < E ? (bf16_order_key(raw[i]) << 16) | (uint32_t)(0xffff - e) : 0u;
+  }
+#pragma unroll
+  for (int w = 1; w < EPL; ++w)  // insertion network, descending
+#pragma unroll
+    for (int i = w; i > 0; --i) {
+      const uint32_t hi = max(key[i - 1], key[i]), lo = min(key[i - 1], key[i]);
+      key[i - 1] = hi;
+      key[i] = lo;
+    }
+  // k + 1 rounds: lane j keeps the j-th key (lane k: the first one not selected)
+  const int rounds = min(k + 1, E);
+  uint32_t sel = 0u;
+  uint32_t top = 0u;
+  for (int j = 0; j < rounds; ++j) {
+    const uint32_t m = wave_max_u32(key[0]);
+    if (j == 0) top = m;
+    const bool win = key[0] == m;  // keys are distinct: exactly one lane
+#pragma unroll
+    for (int i = 0; i + 1 < EPL; ++i) key[i] = win ? key[i + 1] : key[i];
+    if (win) key[EPL - 1] = 0u;
+    if (lane == j) sel = m;
+  }
+  const float mz = bf_bits2f(bf16_from_order_key(top >> 16));
+  float p[EPL];
   float s = 0.f;
 #pragma unroll
   for (int i = 0; i < EPL; ++i) {
     int e = lane + kWave * i;
-    p[i] = e < E ? expf(p[i] - m) : 0.f;
+    p[i] = e < E ? expf(bf_bits2f(raw[i]) - mz) : 0.f;
     s += p[i];
   }
   s = wave_sum(s);
-#pragma unroll
-  for (int i = 0; i < EPL; ++i) {
-    int e = lane + kWave * i;
-    p[i] = e < E ? p[i] / s : -1.0f;
-  }
-  float tot = 0.f;
-  float mine_p = 0.f;
+  // p of the selected entries, with the same operations as every other entry's
+  const uint32_t zb = bf16_from_order_key(sel >> 16);
+  const float ps = expf(bf_bits2f(zb) - mz) / s;
+  const float pn = __shfl_down(ps, 1);
+  const uint32_t kn = (uint32_t)__shfl_down((int)sel, 1);
+  bool bad = false;
+  if (lane + 1 < rounds) bad = !(ps > pn) && (sel >> 16) != (kn >> 16);
+  // boundary entry: its logit at least 2^-10 in magnitude (distinct bf16 logits near it then
+  // differ by >= 2^-18, >= 16 ulps of exp) and its p a normal number
+  if (lane == k && lane < rounds) bad = !(fabsf(bf_bits2f(zb)) >= 0x1p-10f) || !(ps >= 0x1p-100f);
+  float mine_p = 0.f, tot = 0.f;
   int mine_i = 0;
-  for (int j = 0; j < k; ++j) {
-    float bp = -2.0f;
-    int bi = 0x7fffffff;
+  if (__ballot(bad) == 0ull) {
+    mine_p = ps;
+    mine_i = 0xffff - (int)(sel & 0xffffu);
+    for (int j = 0; j < k; ++j)  // sequential j order
+      tot += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ps), j));
+  } else {
 #pragma unroll
-    for (int i = 0; i < EPL; ++i)
-      if (p[i] > bp) {  // strict: the lowest expert of the lane wins a tie
-        bp = p[i];
-        bi = lane + kWave * i;
-      }
-    wave_argmax(bp, bi);
-#pragma unroll
-    for (int i = 0; i < EPL; ++i)
-      if (lane + kWave * i == bi) p[i] = -1.0f;
-    tot += bp;  // sequential j order
-    if (lane == j) {
-      mine_p = bp;
-      mine_i = bi;
+    for (int i = 0; i < EPL; ++i) {
+      int e = lane + kWave * i;
+      p[i] = e < E ? p[i] / s : -1.0f;
     }
+    route_select_exact<EPL>(p, E, k, lane, mine_p, mine_i, tot);
   }
   my_idx = mine_i;
   my_w = mine_p / tot;

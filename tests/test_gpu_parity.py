@@ -48,6 +48,45 @@ def test_route_bitexact(pkg, dev, E, k, seed):
     assert torch.equal(counts.cpu(), torch.bincount(ref_i.reshape(-1), minlength=E).int())
 
 
+def _hard_rows(E, g):
+    """Rows where the largest logits are not the largest p in their order: exp underflow
+    (p = 0 for distinct logits), subnormal boundary p, tiny logits at the selection
+    boundary, exact logit ties, and ordinary rows between them."""
+    rows = []
+    r = torch.zeros(E)
+    r[:3] = 100.0
+    r[3:] = -200.0 - torch.arange(E - 3) * 0.5  # p underflows to 0 for distinct logits
+    rows.append(r)
+    r = torch.full((E,), -60.0)
+    r[:2] = 40.0
+    r[5::7] = -60.5  # subnormal p at the boundary
+    rows.append(r)
+    r = torch.randn(E, generator=g) * 1e-4  # every logit under 2^-10
+    r[:4] = 2.0
+    rows.append(r)
+    r = torch.randn(E, generator=g)
+    r[E // 2:] = r[: E - E // 2].clone()  # pairs of equal logits
+    rows.append(r)
+    r = torch.zeros(E)  # all tied
+    rows.append(r)
+    r = torch.randn(E, generator=g) * 30  # wide spread, no special structure
+    rows.append(r)
+    return torch.stack(rows).to(BF16)
+
+
+@pytest.mark.parametrize("E,k", [(256, 8), (64, 8), (16, 4)])
+def test_route_hard_rows(pkg, dev, E, k):
+    """The exact-selection fallback of the routing kernel on rows built to need it."""
+    g = torch.Generator().manual_seed(E + k)
+    logits = torch.cat([_hard_rows(E, g), router_rows(16, E, 3)])
+    w, i, _ = pkg.ops.route(logits.to(dev), k)
+    torch.cuda.synchronize()
+    ref_w, ref_i = orc.route(logits, k)
+    assert torch.equal(i.cpu(), ref_i)
+    diff = (w.float().cpu() - ref_w.float()).abs()
+    assert (diff <= ref_w.float().abs() * 2.0 ** -7 + 1e-30).all()
+
+
 def test_route_bruteforce_small(pkg, dev):
     logits = router_rows(16, 8, 7)
     _, i, _ = pkg.ops.route(logits.to(dev), 3)
