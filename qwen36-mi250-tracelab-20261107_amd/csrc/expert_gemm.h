@@ -57,6 +57,7 @@ struct GemmArgs {
   const int* order;  // sorted row -> pair
   int topk, P, E, T;
   int nrb;           // weight-row blocks per tile (set by the launcher)
+  int MTgrid;        // tiles the grid covers (set by the launcher)
   int dbg;           // 0; tuning experiments only (MOE_GEMM_DEBUG): 1 skip token-row
                      // loads, 2 skip MFMAs, 4 skip per-chunk barriers
   int fuse;          // kFuseNone / kFuseRouteSort / kFuseCombine

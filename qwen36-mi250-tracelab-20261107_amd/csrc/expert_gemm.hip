@@ -24,7 +24,7 @@
 //   16 rows per load instruction; a ring of NA chunks of KC k-values is kept in flight.
 // * B operand (token rows): the WR waves of a K slice stage each chunk of the tile's token
 //   rows in LDS with row-contiguous 256-byte loads (four rows per instruction), double
-//   buffered, and read it back in the MFMA B layout (conflict-free: 272-byte row pitch).
+//   buffered, and read it back in the MFMA B layout (row pitch padded by 16-32 bytes).
 // fp8-e4m3 weights (per-output-row fp32 scales) are converted to bf16 in registers (exact)
 // and the scale multiplies the fp32 accumulator before the bf16 rounding:
 // sum_k s_n q_nk x_k = s_n sum_k q_nk x_k.
@@ -42,7 +42,8 @@ namespace moe {
 template <int MODE, int WR, int WK, int TOKB, bool HAS_FP8, int KC, int R = 4, int FUSE = 0>
 __global__ __launch_bounds__(64 * WR * WK) void k_expert_gemm(GemmArgs args) {
   constexpr int kRowU4 = KC / 8;        // uint4 per staged token-row chunk (bf16)
-  constexpr int kPitchU4 = kRowU4 + 1;  // LDS row pitch in uint4 (conflict-free B reads)
+  // LDS row pitch in uint4: +2 for 128-byte rows, +1 for longer ones (measured fastest)
+  constexpr int kPitchU4 = kRowU4 + (kRowU4 == 8 ? 2 : 1);
   constexpr int LPC16 = KC / 32;        // bf16 weight loads per lane per chunk
   constexpr int LPC8 = KC / 64;         // fp8 weight loads per lane per chunk
   constexpr int LPCA = LPC16;           // ring entries per chunk (fp8 uses LPC8 of them)
@@ -493,7 +494,7 @@ hipError_t launch_expert_gemm(int mode, int role, int bm, const GemmArgs& a_in, 
     if (!fits(c, mode, a.op[0]) || !fits(c, mode, a.op[1])) continue;
     // the fused route + sort runs in one workgroup: one thread per expert at least
     if (a.fuse == kFuseRouteSort && 64 * c.wr * c.wk < a.f.E) continue;
-    if (c.wk * 2 * c.tokb * 16 * (c.kc / 8 + 1) * 16 > 65536) continue;
+    if (c.wk * 2 * c.tokb * 16 * (c.kc / 8 + (c.kc == 64 ? 2 : 1)) * 16 > 65536) continue;
     int rows = (mode == kModeSwiglu ? 8 : 16) * c.wr;
     int nmax = a.op[0].N > a.op[1].N ? a.op[0].N : a.op[1].N;
     a.nrb = nmax / rows;

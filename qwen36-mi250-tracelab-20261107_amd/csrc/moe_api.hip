@@ -312,7 +312,13 @@ hipError_t launch_router(const void* x, int T, int H, const void* w_pack, int n_
     a.f = *fa;
   }
   // 16-token tiles with K split over 4 waves: the most waves for a 1 MiB weight.
-  const int bm = 16;
+  int bm = 16;
+  if (const char* env = getenv("MOE_ROUTER_BM")) bm = atoi(env);
+  if (bm == prefill_tile_rows() && !fa) {
+    hipError_t err = launch_prefill_gemm(kModePlain, a, (T + bm - 1) / bm, st);
+    if (err != hipErrorInvalidValue) return err;
+    bm = 16;
+  }
   return launch_expert_gemm(kModePlain, kRoleRouter, bm, a, (T + bm - 1) / bm, st);
 }
 }  // namespace
