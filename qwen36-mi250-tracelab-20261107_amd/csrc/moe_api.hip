@@ -311,8 +311,10 @@ hipError_t launch_router(const void* x, int T, int H, const void* w_pack, int n_
     a.fuse = kFuseRouteSort;
     a.f = *fa;
   }
-  // 16-token tiles with K split over 4 waves: the most waves for a 1 MiB weight.
-  int bm = 16;
+  // Token rows per tile: 16-token tiles (K split over 8 waves) give the most waves for a
+  // handful of tokens; larger batches re-read the 1 MiB weight once per tile, so their
+  // tiles grow with T (measured: 16 up to 64 tokens, 32 up to 1024, 64 above).
+  int bm = T <= 64 ? 16 : (T <= 1024 ? 32 : 64);
   if (const char* env = getenv("MOE_ROUTER_BM")) bm = atoi(env);
   if (bm == prefill_tile_rows() && !fa) {
     hipError_t err = launch_prefill_gemm(kModePlain, a, (T + bm - 1) / bm, st);

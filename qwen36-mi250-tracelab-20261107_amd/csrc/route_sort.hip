@@ -79,21 +79,36 @@ __global__ __launch_bounds__(kSortThreads) void k_sort_scan(int* __restrict__ bc
   __shared__ int hist[kMaxE];
   __shared__ int offs[kMaxE];
   __shared__ int tmp[kSortWaves + 1];
+  // Per-expert exclusive scan over the blocks. The block counts are read in groups of 16
+  // whose loads are all in flight together (one memory round trip per group, not per block).
+  constexpr int G = 16;
   int e = threadIdx.x;
   if (e < E) {
     int acc = 0;
-    for (int b = 0; b < nblocks; ++b) {
-      int c = bcnt[(long long)b * E + e];
-      bcnt[(long long)b * E + e] = acc;
-      acc += c;
+    for (int b0 = 0; b0 < nblocks; b0 += G) {
+      int c[G];
+#pragma unroll
+      for (int i = 0; i < G; ++i) c[i] = b0 + i < nblocks ? bcnt[(long long)(b0 + i) * E + e] : 0;
+#pragma unroll
+      for (int i = 0; i < G; ++i) {
+        if (b0 + i < nblocks) bcnt[(long long)(b0 + i) * E + e] = acc;
+        acc += c[i];
+      }
     }
     hist[e] = acc;
   }
   __syncthreads();
   build_table(hist, E, P, T, bm, has_shared, offs, counts_g, offsets_g, table, MT, tmp);
   if (e < E) {
-    int o = offs[e];
-    for (int b = 0; b < nblocks; ++b) bcnt[(long long)b * E + e] += o;
+    const int o = offs[e];
+    for (int b0 = 0; b0 < nblocks; b0 += G) {
+      int c[G];
+#pragma unroll
+      for (int i = 0; i < G; ++i) c[i] = b0 + i < nblocks ? bcnt[(long long)(b0 + i) * E + e] : 0;
+#pragma unroll
+      for (int i = 0; i < G; ++i)
+        if (b0 + i < nblocks) bcnt[(long long)(b0 + i) * E + e] = c[i] + o;
+    }
   }
 }
 
@@ -131,6 +146,9 @@ size_t sort_scratch_bytes(int P, int E) {
 
 bool sort_uses_small(int P, int E) { return P <= kSmallMaxPairs && E <= kSmallMaxE; }
 
+// Up to this many tokens the one-workgroup kernel also routes (fewer launches).
+constexpr int kRouteSortFusedMaxTokens = 16;
+
 // Route (when logits) and sort. ids (int32 or int64) are read when logits is null,
 // written (idx64/idx32/w_out) when logits is given.
 hipError_t launch_route_sort(const uint16_t* logits, long long ld, const int* ids32_in,
@@ -139,6 +157,15 @@ hipError_t launch_route_sort(const uint16_t* logits, long long ld, const int* id
                              int* offsets, int* order, int* table, int MT, int* scratch,
                              hipStream_t s) {
   const int P = T * k;
+  if (logits && sort_uses_small(P, E) && T > kRouteSortFusedMaxTokens) {
+    // one wave per token across many workgroups, then the one-workgroup sort: faster than
+    // routing all tokens inside the sorting workgroup once there are more than a few
+    hipError_t err = launch_route(logits, ld, T, E, k, idx64, idx32, w_out, nullptr, s);
+    if (err != hipSuccess) return err;
+    return launch_route_sort(nullptr, 0, idx32 ? idx32 : nullptr, idx32 ? nullptr : idx64, T, E,
+                             k, bm, has_shared, nullptr, nullptr, nullptr, counts, offsets, order,
+                             table, MT, scratch, s);
+  }
   if (sort_uses_small(P, E)) {
     // one workgroup; a few tokens need few waves (fewer barriers to wait at)
     int need = P > E ? P : E;
