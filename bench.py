@@ -259,6 +259,98 @@ def cpu_baseline(torch, seconds):
     }
 
 
+def head_name(results):
+    return "c2" if "c2" in results else next(iter(results))
+
+
+TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic.json"
+
+
+def measured_traffic(kernel, config):
+    """HBM bytes per launch of ``kernel`` on ``config`` from the committed counter summary
+    (two rocprofv3 --pmc runs, summarised by --pmc-summary), or None."""
+    try:
+        data = json.loads(TRAFFIC_FILE.read_text())
+    except (OSError, ValueError):
+        return None
+    # the largest launch of that kernel family on that workload (the gate_up of the block)
+    recs = [v for k, v in data.items()
+            if k.startswith(f"{config}:moe::{kernel}<") and isinstance(v, dict)]
+    if not recs:
+        return None
+    rec = max(recs, key=lambda v: v["hbm_bytes_per_launch"])
+    return {"bytes_per_launch": rec["hbm_bytes_per_launch"],
+            "source": f"profiles/{TRAFFIC_FILE.name} ({rec['command']})"}
+
+
+def _pmc_rows(d, counter):
+    import csv
+    import glob
+
+    out = {}
+    for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+        for r in csv.DictReader(open(f)):
+            if r["Counter_Name"] != counter:
+                continue
+            name = r["Kernel_Name"]
+            out.setdefault(name, []).append(float(r["Counter_Value"]))
+    return out
+
+
+def pmc_summary(fetch_dir, write_dir, copy_mib, config):
+    """FETCH_SIZE / WRITE_SIZE (KiB per dispatch, as rocprofv3 reports them) of each moe::
+    kernel, scaled by the counter's reading for the plain copy of ``copy_mib`` MiB, which
+    reads and writes exactly that many bytes. Writes profiles/hbm_traffic.json and a
+    markdown table."""
+    fetch = _pmc_rows(fetch_dir, "FETCH_SIZE")
+    write = _pmc_rows(write_dir, "WRITE_SIZE")
+    n = copy_mib << 20
+
+    def copy_of(rows):
+        # the device-to-device copy of the calibration (torch copy_ -> HIP's copy kernel)
+        cands = [(k, v) for k, v in rows.items() if "copybuffer" in k.lower()]
+        k, v = max(cands, key=lambda kv: max(kv[1]))
+        return k, max(v) * 1024.0
+
+    ck, cf = copy_of(fetch)
+    _, cw = copy_of(write)
+    f_fac, w_fac = n / cf, n / cw
+    cmd_base = (f"rocprofv3 --pmc {{}} --output-format csv -- python3 bench.py --calibrate-copy "
+                f"{copy_mib} --configs {config} --no-cpu --steps 16 --warmup 16")
+    data = {"copy_kernel": ck, "copy_bytes": n, "fetch_factor": f_fac, "write_factor": w_fac}
+    lines = [f"# HBM traffic per launch ({config}), from FETCH_SIZE and WRITE_SIZE\n",
+             "Commands (from the repository root on one MI355X; one counter per run):\n",
+             "    " + cmd_base.format("FETCH_SIZE"), "    " + cmd_base.format("WRITE_SIZE"),
+             f"    python3 bench.py --pmc-summary <fetch_dir> <write_dir> --pmc-copy-mib {copy_mib} "
+             f"--pmc-config {config}\n",
+             f"Calibration: the plain copy of {copy_mib} MiB (`{ck[:60]}`) reads {cf / 2**20:.1f} "
+             f"MiB by FETCH_SIZE and writes {cw / 2**20:.1f} MiB by WRITE_SIZE: the counters are "
+             f"scaled by {f_fac:.3f} (fetch) and {w_fac:.3f} (write).\n",
+             "| kernel | launches | fetch MB | write MB | HBM MB per launch |", "|---|---|---|---|---|"]
+    for k in sorted(fetch):
+        if "moe::" not in k:
+            continue
+        fv = sum(fetch[k]) / len(fetch[k]) * 1024.0 * f_fac
+        wv = sum(write.get(k, [0.0])) / max(1, len(write.get(k, []))) * 1024.0 * w_fac
+        short = k.replace("void ", "").split("(")[0]
+        data[f"{config}:{short}"] = {"kernel": short, "fetch_bytes": fv, "write_bytes": wv,
+                                      "hbm_bytes_per_launch": int(fv + wv),
+                                      "command": cmd_base.format("FETCH_SIZE|WRITE_SIZE")}
+        lines.append(f"| `{short}` | {len(fetch[k])} | {fv / 1e6:.2f} | {wv / 1e6:.2f} | "
+                     f"{(fv + wv) / 1e6:.2f} |")
+    prev = {}
+    try:
+        prev = json.loads(TRAFFIC_FILE.read_text())
+    except (OSError, ValueError):
+        pass
+    prev.update(data)
+    TRAFFIC_FILE.parent.mkdir(exist_ok=True)
+    TRAFFIC_FILE.write_text(json.dumps(prev, indent=1, sort_keys=True) + "\n")
+    md = ROOT / "profiles" / f"hbm_traffic_{config}.md"
+    md.write_text("\n".join(lines) + "\n")
+    print(md.read_text())
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -268,7 +360,18 @@ def main():
     ap.add_argument("--layers", type=int, default=16)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="first run a plain device copy of MIB MiB (the known-size kernel the "
+                         "FETCH_SIZE / WRITE_SIZE counters are scaled by)")
+    ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="summarise two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) of "
+                         "`bench.py --calibrate-copy M --configs c` into profiles/ and exit")
+    ap.add_argument("--pmc-copy-mib", type=int, default=256)
+    ap.add_argument("--pmc-config", default="c2")
     args = ap.parse_args()
+    if args.pmc_summary:
+        pmc_summary(args.pmc_summary[0], args.pmc_summary[1], args.pmc_copy_mib, args.pmc_config)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (the MoE block runs "
               "on one GPU with no TP/EP exchange); run with --gpus 1", file=sys.stderr)
@@ -283,6 +386,14 @@ def main():
     pkg = load_pkg()
     pkg._lib.load()
     cfgs = [c.strip() for c in args.configs.split(",") if c.strip()]
+    if args.calibrate_copy:
+        n = args.calibrate_copy << 20
+        src = torch.ones(n, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     results = {}
     if "c2" in cfgs:
         results["c2"] = run_config(torch, dev, "c2", 1, args.layers, args.steps, args.warmup)
@@ -299,6 +410,7 @@ def main():
     cpu = None if args.no_cpu else cpu_baseline(torch, args.cpu_seconds)
     kbytes, kus = head["gate_up_bytes"], head["gate_up_us"]
     achieved = kbytes / (kus * 1e-6) / 1e9
+    traffic = measured_traffic(head["gate_up_kernel"], head_name(results))
     line = {
         "metric": METRIC,
         "value": head["us_per_layer"],
@@ -320,7 +432,9 @@ def main():
         "tokens_per_s": head["tokens_per_s"],
         "roofline": {"bound": "hbm", "kernel": head["gate_up_kernel"],
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": traffic["bytes_per_launch"] if traffic else None,
+                     "traffic_source": traffic["source"] if traffic else None,
                      "bytes_per_launch": kbytes, "us_per_launch": kus},
         "cpu_baseline": cpu,
         "configs": results,
