@@ -46,7 +46,7 @@ __global__ __launch_bounds__(64 * WR * WK) void k_expert_gemm(GemmArgs args) {
   constexpr int kPitchU4 = kRowU4 + (kRowU4 == 8 ? 2 : 1);
   constexpr int LPC16 = KC / 32;        // bf16 weight loads per lane per chunk
   constexpr int LPC8 = KC / 64;         // fp8 weight loads per lane per chunk
-  constexpr int LPCA = LPC16;           // ring entries per chunk (fp8 uses LPC8 of them)
+  constexpr int LPCA = HAS_FP8 ? LPC8 : LPC16;  // ring entries per chunk (16-byte loads)
   static_assert(!HAS_FP8 || LPC8 >= 1, "fp8 needs KC >= 64");
   constexpr int kOutRowsPerWG = (MODE == kModeSwiglu ? 8 : 16) * WR;
   constexpr int BM = 16 * TOKB;
@@ -138,10 +138,11 @@ __global__ __launch_bounds__(64 * WR * WK) void k_expert_gemm(GemmArgs args) {
   const uint16_t* __restrict__ xin = op.in;
 #pragma unroll
   for (int i = 0; i < STG; ++i) srow[i] = srow[i] * op.ld_in + kbeg + part * 8;
-  // Rows past the tile's last 16-row block are not needed.
   bool sneed[STG];
 #pragma unroll
-  for (int i = 0; i < STG; ++i) sneed[i] = ((i * WR + wr) * RPI) < ntb * 16;
+  for (int i = 0; i < STG; ++i) sneed[i] = (i * WR + wr) * RPI + qlane < r1 - r0;
+  // Only the tile's real token rows are staged: the LDS rows past them keep stale data,
+  // which reaches only MFMA output columns that are never stored.
   uint4* bsl = lds + wk * 2 * kBufU4;  // this K slice's two buffers
   auto stage_slot = [&](int i) { return ((i * WR + wr) * RPI + qlane) * kPitchU4 + part; };
 
@@ -374,6 +375,11 @@ hipError_t launch_cfg(const Cfg& c, const GemmArgs& a, int grid, hipStream_t st)
   }
   if constexpr (HAS_FP8) {
     MOE_L(4, 1, 2, 256, 2)
+    MOE_L(2, 2, 2, 256, 2)
+    MOE_L(4, 2, 2, 256, 2)
+    MOE_L(4, 1, 2, 256, 3)
+    MOE_L(2, 1, 2, 256, 2)
+    MOE_L(8, 1, 2, 256, 2)
     MOE_L(4, 1, 2, 128, 4)
     MOE_L(1, 4, 1, 64, 8)
     MOE_L(2, 2, 2, 64, 8)

@@ -6,6 +6,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <mutex>
 #include <string>
 
 #include "../../include/moe_mi355x.h"
@@ -168,18 +169,65 @@ GemmOperand down_operand(const void* down, const float* scale, int H, int I, con
 // One launch for the routed experts and the shared expert, or two when their weight types
 // differ (fp8 experts, bf16 shared expert): the shared expert's tiles then come from the
 // token count alone (rows P .. P + T), not from the table.
+// A second stream per device for work that can run beside the caller's stream (forked and
+// joined with events, so it is ordered with the caller's work and is captured into the
+// caller's HIP graph as a parallel branch). Created on first use outside graph capture;
+// while none exists the work runs on the caller's stream. Default priority.
+struct AuxStream {
+  hipStream_t s = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
+};
+AuxStream* aux_stream(hipStream_t caller) {
+  static std::mutex mu;
+  static AuxStream per_device[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  std::lock_guard<std::mutex> lock(mu);
+  AuxStream& a = per_device[dev];
+  if (a.s) return &a;
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(caller, &st) != hipSuccess || st != hipStreamCaptureStatusNone)
+    return nullptr;
+  if (hipStreamCreateWithFlags(&a.s, hipStreamNonBlocking) != hipSuccess) {
+    a.s = nullptr;
+    return nullptr;
+  }
+  if (hipEventCreateWithFlags(&a.fork, hipEventDisableTiming) != hipSuccess ||
+      hipEventCreateWithFlags(&a.join, hipEventDisableTiming) != hipSuccess) {
+    hipStreamDestroy(a.s);
+    a.s = nullptr;
+    return nullptr;
+  }
+  return &a;
+}
+
+// A launch whose routed experts are fp8 and shared expert bf16 runs as two launches (each
+// kernel is compiled for one weight type); the shared one goes to the auxiliary stream so
+// the two overlap.
 hipError_t launch_split(int mode, int role, int bm, const GemmArgs& a, int MT, hipStream_t s) {
   if (a.op[0].N <= 0 || a.op[1].N <= 0 || a.op[0].fp8 == a.op[1].fp8)
     return launch_expert_gemm(mode, role, bm, a, MT, s);
-  GemmArgs r = a;
-  r.op[1].N = 0;
-  hipError_t err = launch_expert_gemm(mode, role, bm, r, MT, s);
-  if (err != hipSuccess) return err;
   GemmArgs v = a;
   v.op[0] = v.op[1];
   v.op[0].N = 0;
   v.table = nullptr;
-  return launch_expert_gemm(mode, role, bm, v, (a.T + bm - 1) / bm, s);
+  AuxStream* aux = aux_stream(s);
+  hipStream_t vs = s;
+  if (aux) {
+    hipError_t e = hipEventRecord(aux->fork, s);
+    if (e == hipSuccess) e = hipStreamWaitEvent(aux->s, aux->fork, 0);
+    if (e != hipSuccess) return e;
+    vs = aux->s;
+  }
+  hipError_t err = launch_expert_gemm(mode, role, bm, v, (a.T + bm - 1) / bm, vs);
+  if (err != hipSuccess) return err;
+  GemmArgs r = a;
+  r.op[1].N = 0;
+  err = launch_expert_gemm(mode, role, bm, r, MT, s);
+  if (err != hipSuccess || !aux) return err;
+  err = hipEventRecord(aux->join, aux->s);
+  if (err == hipSuccess) err = hipStreamWaitEvent(s, aux->join, 0);
+  return err;
 }
 
 int run_gate_up(const void* x, int T, int H, int E, int k, int I, const void* gate_up,
