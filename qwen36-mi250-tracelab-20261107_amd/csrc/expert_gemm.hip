@@ -40,7 +40,9 @@ namespace moe {
 
 // KC: K elements per chunk (128; 32 for small test shapes, bf16 only); R: chunks in flight.
 template <int MODE, int WR, int WK, int TOKB, bool HAS_FP8, int KC, int R = 4, int FUSE = 0>
-__global__ __launch_bounds__(64 * WR * WK) void k_expert_gemm(GemmArgs args) {
+__global__ __launch_bounds__(64 * WR * WK)
+__attribute__((amdgpu_waves_per_eu(TOKB <= 2 && KC >= 64 ? 3 : 1)))
+void k_expert_gemm(GemmArgs args) {
   constexpr int kRowU4 = KC / 8;        // uint4 per staged token-row chunk (bf16)
   // LDS row pitch in uint4: +2 for 128-byte rows, +1 for longer ones (measured fastest)
   constexpr int kPitchU4 = kRowU4 + (kRowU4 == 8 ? 2 : 1);
@@ -188,35 +190,26 @@ __global__ __launch_bounds__(64 * WR * WK) void k_expert_gemm(GemmArgs args) {
       const int c = c0 + cc;
       if (c >= nch) break;
       const uint4* bcur = bsl + (c & 1) * kBufU4;
-      uint4 a4[LPC16];
-      if (!use_fp8) {
+      // one ring entry at a time (bf16: one k-step; fp8: 16 bytes -> two k-steps), so only
+      // the fragments of that entry are live
 #pragma unroll
-        for (int s = 0; s < LPC16; ++s) a4[s] = aring[cc][s];
-      } else if (HAS_FP8) {
+      for (int s = 0; s < LPCA; ++s) {
+        uint4 a0, a1;
+        if (use_fp8)
+          fp8x16_to_bf16(aring[cc][s], a0, a1);
+        else
+          a0 = aring[cc][s];
 #pragma unroll
-        for (int s = 0; s < LPC8; ++s) fp8x16_to_bf16(aring[cc][s], a4[2 * s], a4[2 * s + 1]);
-      }
-#pragma unroll
-      for (int tb = 0; tb < TOKB; ++tb) {
-        if (tb < ntb) {
-          const uint4* brow = bcur + (tb * 16 + lr) * kPitchU4;
-          uint4 b[LPC16];
-          if (!use_fp8) {
-#pragma unroll
-            for (int s = 0; s < LPC16; ++s) b[s] = brow[s * 4 + kq];
-          } else if (HAS_FP8) {
-            // fp8 A lane kq holds k = s2*64 + kq*16 + h*8 (+0..7)
-#pragma unroll
-            for (int s2 = 0; s2 < LPC8; ++s2)
-#pragma unroll
-              for (int h = 0; h < 2; ++h) b[s2 * 2 + h] = brow[s2 * 8 + kq * 2 + h];
-          }
-          if (!(args.dbg & 2)) {
-#pragma unroll
-            for (int s = 0; s < LPC16; ++s) acc[tb] = mfma16x16x32(a4[s], b[s], acc[tb]);
-          } else {
-#pragma unroll
-            for (int s = 0; s < LPC16; ++s) acc[tb][0] += __uint_as_float(a4[s].x ^ b[s].y);
+        for (int tb = 0; tb < TOKB; ++tb) {
+          if (tb < ntb) {
+            const uint4* brow = bcur + (tb * 16 + lr) * kPitchU4;
+            if (use_fp8) {
+              // fp8 A lane kq holds k = s*64 + kq*16 + h*8 (+0..7)
+              acc[tb] = mfma16x16x32(a0, brow[s * 8 + kq * 2], acc[tb]);
+              acc[tb] = mfma16x16x32(a1, brow[s * 8 + kq * 2 + 1], acc[tb]);
+            } else {
+              acc[tb] = mfma16x16x32(a0, brow[s * 4 + kq], acc[tb]);
+            }
           }
         }
       }
@@ -377,7 +370,6 @@ hipError_t launch_cfg(const Cfg& c, const GemmArgs& a, int grid, hipStream_t st)
     MOE_L(4, 1, 2, 256, 2)
     MOE_L(2, 2, 2, 256, 2)
     MOE_L(4, 2, 2, 256, 2)
-    MOE_L(4, 1, 2, 256, 3)
     MOE_L(2, 1, 2, 256, 2)
     MOE_L(8, 1, 2, 256, 2)
     MOE_L(4, 1, 2, 128, 4)
