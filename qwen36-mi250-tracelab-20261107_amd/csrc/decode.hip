@@ -24,6 +24,8 @@
 // 512 B (fp8) of one row contiguously; partial sums are reduced with DPP in a fixed order.
 // Rounding points are those of the tiled kernels (rbf after each projection, SwiGLU as
 // bf16(bf16(silu(bf16 g)) * bf16 u), combine terms bf16(w * y) under round_w).
+#include <stdlib.h>
+
 #include "moe_common.h"
 #include "route_sort_dev.h"
 #include "decode.h"
@@ -359,6 +361,82 @@ __global__ __launch_bounds__(kDecThreads) void k_dec_down(DecodeArgs a) {
   }
 }
 
+// One token (T = 1, k <= 15): wave j < k owns pair j and wave k the shared expert; each
+// wave streams kDownRows consecutive rows of its expert's down projection (contiguous
+// memory) against its one activation row, and the combine runs over the waves' results in
+// LDS in routing order. grid: H / kDownRows workgroups of (k + 1) waves.
+constexpr int kDownRows = 8;
+template <int IC, bool FP8>
+__global__ __launch_bounds__(1024) void k_dec_down1(DecodeArgs a) {
+  __shared__ float s_term[16][kDownRows];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int n0 = blockIdx.x * kDownRows;
+  const int I = IC * 512;
+  const int H = a.H;
+  const bool is_shared = wave == a.k;
+  if (is_shared && a.sh_down) {
+    // the shared expert: no routing dependency
+    uint4 xs[2], ws[kDownRows][2];
+    const int isc = a.IS / 512;
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+      if (c < isc) {
+#pragma unroll
+        for (int r = 0; r < kDownRows; ++r)
+          ws[r][c] = ld16_stream(a.sh_down + (long long)(n0 + r) * a.IS + c * 512 + lane * 8);
+        xs[c] = ld16(a.act_sh + c * 512 + lane * 8);
+      }
+#pragma unroll
+    for (int r = 0; r < kDownRows; ++r) {
+      float d = 0.f;
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+        if (c < isc) d = dot8(ws[r][c], xs[c], d);
+      d = wave_sum(d);
+      if (lane == r) s_term[15][r] = rbf(d);
+    }
+  } else if (!is_shared) {
+    const int e = a.idx32[wave];
+    const float w = bf_bits2f(a.wts[wave]);
+    WFrag<FP8> wf[kDownRows][IC];
+    uint4 av[IC];
+#pragma unroll
+    for (int c = 0; c < IC; ++c) av[c] = ld16(a.act + (long long)wave * I + c * 512 + lane * 8);
+#pragma unroll
+    for (int r = 0; r < kDownRows; ++r) {
+      const void* row = wrow<FP8>(a.down, (long long)e * H + n0 + r, I);
+#pragma unroll
+      for (int c = 0; c < IC; ++c) wf[r][c] = ldraw<FP8>(row, c * 512 + lane * 8);
+    }
+    float scl = 1.f;
+    const float* sc = a.dn_scale ? a.dn_scale + (long long)e * H + n0 : nullptr;
+#pragma unroll
+    for (int r = 0; r < kDownRows; ++r) {
+      float d = 0.f;
+#pragma unroll
+      for (int c = 0; c < IC; ++c) d = dot8(decode<FP8>(wf[r][c]), av[c], d);
+      d = wave_sum(d);
+      if (sc) scl = sc[r];
+      const float y = rbf(d * scl);
+      if (lane == r) s_term[wave][r] = a.round_w ? rbf(w * y) : w * y;
+    }
+  }
+  __syncthreads();
+  if (wave == 0 && lane < kDownRows) {
+    const int n = n0 + lane;
+    float acc = 0.f;
+    for (int j = 0; j < a.k; ++j) acc += s_term[j][lane];  // routing order j
+    float o = rbf(acc);
+    if (a.sh_down) {
+      const float gte = rbf(sigmoidf_(bf_bits2f(a.logits[a.E])));
+      o = rbf(o + rbf(gte * s_term[15][lane]));
+    }
+    if (a.residual) o += bf_bits2f(a.residual[n]);
+    a.out[n] = f2bf_bits(o);
+  }
+}
+
 // ------------------------------------------------------------------------ host side
 
 bool decode_fits(const DecodeArgs& a) {
@@ -371,6 +449,12 @@ bool decode_fits(const DecodeArgs& a) {
 }
 
 namespace {
+
+// MOE_DECODE_DOWN=rows: the wave-per-row down kernel for one token too (comparisons).
+bool down_legacy() {
+  const char* env = getenv("MOE_DECODE_DOWN");
+  return env && env[0] == 'r';
+}
 
 template <int NT>
 hipError_t launch_router_nt(const DecodeArgs& a, hipStream_t s) {
@@ -406,6 +490,17 @@ hipError_t launch_gate_up_nt(const DecodeArgs& a, hipStream_t s) {
 
 template <int NT, bool FP8>
 hipError_t launch_down_nt(const DecodeArgs& a, hipStream_t s) {
+  if (NT == 1 && a.T == 1 && a.k <= 15 && a.H % kDownRows == 0 && !down_legacy()) {
+    const int grid = a.H / kDownRows;
+    const dim3 block(64 * (a.k + 1));
+    if (a.I == 512)
+      hipLaunchKernelGGL((k_dec_down1<1, FP8>), dim3(grid), block, 0, s, a);
+    else if (a.I == 1024)
+      hipLaunchKernelGGL((k_dec_down1<2, FP8>), dim3(grid), block, 0, s, a);
+    else
+      return hipErrorInvalidValue;
+    return hipGetLastError();
+  }
   const int grid = a.H / 4;
   if (a.I == 512)
     hipLaunchKernelGGL((k_dec_down<NT, 1, FP8>), dim3(grid), dim3(kDecThreads), 0, s, a);

@@ -175,3 +175,30 @@ def test_decode_stages_compose_to_block(pkg, dev, layer):
     assert torch.equal(idx64, b_idx) and torch.equal(idx32.long(), b_idx)
     assert torch.equal(wts, b_wts)
     assert torch.equal(out, b_out)
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+def test_decode_one_token_down_kernels_agree(pkg, dev, layer, fp8):
+    """One token: the wave-per-pair down kernel and the wave-per-row one compute the same
+    dot products in the same order, so they give the same bits."""
+    mlp = _mlp(layer, dev)
+    if fp8:
+        q, s = pkg.fp8.quantize_rows(layer["gate_up"])
+        q2, s2 = pkg.fp8.quantize_rows(layer["down"])
+        mlp.experts.gate_up_proj, mlp.experts.gate_up_scale = q, s
+        mlp.experts.down_proj, mlp.experts.down_scale = q2, s2
+    g = torch.Generator().manual_seed(77)
+    x = torch.randn(1, 2048, generator=g).to(BF16).to(dev)
+    r = torch.randn(1, 2048, generator=g).to(BF16).to(dev)
+    a = pkg.block.moe(x, mlp, 8, decode=True, residual=r)
+    old = os.environ.get("MOE_DECODE_DOWN")
+    os.environ["MOE_DECODE_DOWN"] = "rows"
+    try:
+        b = pkg.block.moe(x, mlp, 8, decode=True, residual=r)
+    finally:
+        if old is None:
+            os.environ.pop("MOE_DECODE_DOWN", None)
+        else:
+            os.environ["MOE_DECODE_DOWN"] = old
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
