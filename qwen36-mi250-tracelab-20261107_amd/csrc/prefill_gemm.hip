@@ -38,17 +38,20 @@ namespace moe {
 namespace {
 constexpr int PBM = 256;                          // tokens per tile
 constexpr int PBN = 256;                          // weight rows per workgroup
-constexpr int PKC = 32;                           // K elements per chunk
-constexpr int kBlkBytes = 1024;                   // 16 rows x 32 k x 2 B
-constexpr int kBlocks = (PBN + PBM) / 16;         // blocks per stage (A then B)
-constexpr int kStageBytes = kBlocks * kBlkBytes;  // 32 KiB
-constexpr int kStages = 5;
+constexpr int PKC = 32;                           // K elements per MFMA k-step
+constexpr int DKC = 64;                           // K elements per DMA chunk (128-byte rows)
+constexpr int kRowBytes = DKC * 2;                // 128
+constexpr int kBlkBytes = 16 * kRowBytes;         // a 16-row fragment block: 2 KiB
+constexpr int kOpStage = 256 * kRowBytes;         // one operand of one chunk: 32 KiB
+constexpr int kStagesA = 3, kAheadA = 2;          // weight ring: chunk d + 3 loads at step d
+constexpr int kStagesB = 2, kAheadB = 1;          // token-row ring: chunk d + 2
+constexpr int kLdsBytes = (kStagesA + kStagesB) * kOpStage;  // 160 KiB
 constexpr int kThreads = 512;
 constexpr int kXcds = 8;                          // XCDs of an MI355X (round-robin dispatch)
-constexpr int kWaves = kThreads / 64;
-constexpr int kLoadsPerWave = kBlocks / kWaves;   // DMA loads per wave per chunk (4)
-static_assert(kLoadsPerWave == 4, "vmcnt accounting below assumes 4 loads per chunk");
-static_assert(kStages <= 5, "wait_chunks covers up to three younger chunks");
+constexpr int kGroups = 256 / 8;                  // 8-row DMA groups per operand and chunk
+constexpr int kLoadsPerWave = kGroups / (kThreads / 64);  // per operand and chunk: 4
+static_assert(kLoadsPerWave == 4, "wait_loads counts 4 loads per operand per chunk");
+static_assert(kAheadA <= kStagesA - 1 && kAheadB <= kStagesB - 1, "ring slots reused early");
 }  // namespace
 
 typedef unsigned u32x4v __attribute__((ext_vector_type(4)));
@@ -75,11 +78,12 @@ struct Frags {
   u32x4v a[4], b[8];
 };
 
-// Issue the wave's 12 fragment reads of the stage at `base` (+ this lane's unit offset);
-// they complete at frags_ready.
-__device__ __forceinline__ void read_frags(uint32_t base, int wm, int wn, Frags& f) {
-  const uint32_t abase = base + wm * 4 * kBlkBytes;
-  const uint32_t bbase = base + (16 + wn) * kBlkBytes;
+// Issue the wave's 12 fragment reads of one k-step from the A / B stages at astage /
+// bstage (which include this lane's offset for the k-step); they complete at frags_ready.
+__device__ __forceinline__ void read_frags(uint32_t astage, uint32_t bstage, int wm, int wn,
+                                           Frags& f) {
+  const uint32_t abase = astage + wm * 4 * kBlkBytes;
+  const uint32_t bbase = bstage + wn * kBlkBytes;
   f.a[0] = lds_read_frag<0 * kBlkBytes>(abase);
   f.a[1] = lds_read_frag<1 * kBlkBytes>(abase);
   f.a[2] = lds_read_frag<2 * kBlkBytes>(abase);
@@ -110,21 +114,23 @@ __device__ __forceinline__ void mma_frags(const Frags& f, int nb, f32x4_t (&acc)
   }
 }
 
-// Wait until at most `younger` chunks of this wave's DMA loads are still in flight.
-__device__ __forceinline__ void wait_chunks(int younger) {
-  if (younger >= 3)
-    asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
-  else if (younger == 2)
-    asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-  else if (younger == 1)
-    asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
-  else
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+// Wait until at most n (0..12) of this wave's DMA loads are still in flight.
+__device__ __forceinline__ void wait_loads(int n) {
+  switch (n) {
+#define W(N)                                          \
+  case N:                                             \
+    asm volatile("s_waitcnt vmcnt(" #N ")" ::: "memory"); \
+    break;
+    W(12) W(11) W(10) W(9) W(8) W(7) W(6) W(5) W(4) W(3) W(2) W(1)
+#undef W
+    default:
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  }
 }
 
 template <int MODE>
 __global__ __launch_bounds__(kThreads, 1) void k_prefill_gemm(GemmArgs args) {
-  extern __shared__ uint4 smem[];  // [kStages][kBlocks][1 KiB]
+  extern __shared__ uint4 smem[];  // A ring [kStagesA][16][1 KiB], B ring [kStagesB][16][1 KiB]
 
   // XCD-aware order: workgroup b runs on XCD b % 8, so the nrb workgroups of one tile get
   // ids 8 apart (same XCD, dispatched together) and share the tile's token rows in that
@@ -159,54 +165,64 @@ __global__ __launch_bounds__(kThreads, 1) void k_prefill_gemm(GemmArgs args) {
   const int wn = wave >> 2;  // token-block parity
   const int lr = lane & 15;
   const int kq = lane >> 4;
-  const int nch = op.K / PKC;
   const int ntok = r1 - r0;
 
-  // ---- DMA sources: this wave loads blocks wave + 8 i (i < 4) of every stage: A blocks
-  // wave, wave + 8 and B blocks wave, wave + 8. Lane l fills unit l & 3 of row l >> 2 of the
-  // block, i.e. logical 16-byte unit (l & 3) ^ ((row >> 2) & 3) of that row.
-  const int brow = lane >> 2;
-  const int unit = (lane & 3) ^ ((brow >> 2) & 3);
-  const uint16_t* __restrict__ src[kLoadsPerWave];
+  // ---- DMA sources. A chunk of one operand is 256 rows x 128 B (64 k); each load of a wave
+  // fills one 8-row group (1 KiB, 128 contiguous bytes of each row), the wave's groups being
+  // wave + 8 i (i < 4). Lane l fills physical unit l & 7 of row l >> 3 of the group, which
+  // holds logical 16-byte unit (l & 7) ^ (row & 7): the XOR order that keeps the fragment
+  // reads (16 rows, one logical unit) bank-conflict free.
+  const int grow = lane >> 3;
+  const int unit = (lane & 7) ^ grow;
+  const uint16_t* __restrict__ srca[kLoadsPerWave];
+  const uint16_t* __restrict__ srcb[kLoadsPerWave];
   const uint16_t* __restrict__ wbase =
       reinterpret_cast<const uint16_t*>(op.w) + (long long)(routed ? e : 0) * op.estride;
 #pragma unroll
   for (int i = 0; i < kLoadsPerWave; ++i) {
-    const int blk = wave + 8 * i;  // 0..31
-    if (blk < 16) {
-      const int row = blk * 16 + brow;
-      long long wrow;
-      if (MODE == kModeSwiglu) {
-        const int g = rb * (PBN / 2) + (row >> 6) * 32 + (row & 31);  // gate row index
-        wrow = (long long)g * op.ldw + (((row >> 5) & 1) ? op.up_off : 0);
-      } else {
-        wrow = (long long)min(rb * PBN + row, op.N - 1) * op.ldw;  // last block may be partial
-      }
-      src[i] = wbase + wrow + unit * 8;
+    const int row = (wave + 8 * i) * 8 + grow;  // 0..255
+    long long wrow;
+    if (MODE == kModeSwiglu) {
+      const int g = rb * (PBN / 2) + (row >> 6) * 32 + (row & 31);  // gate row index
+      wrow = (long long)g * op.ldw + (((row >> 5) & 1) ? op.up_off : 0);
     } else {
-      const int t = (blk - 16) * 16 + brow;
-      const int r = min(r0 + t, r1 - 1);
-      long long s;
-      if (!routed)
-        s = r - args.P;
-      else if (op.in_map)
-        s = args.order[r] / args.topk;
-      else
-        s = r;
-      src[i] = op.in + s * op.ld_in + unit * 8;
+      wrow = (long long)min(rb * PBN + row, op.N - 1) * op.ldw;  // last block may be partial
     }
+    srca[i] = wbase + wrow + unit * 8;
+    const int r = min(r0 + row, r1 - 1);
+    long long src;
+    if (!routed)
+      src = r - args.P;
+    else if (op.in_map)
+      src = args.order[r] / args.topk;
+    else
+      src = r;
+    srcb[i] = op.in + src * op.ld_in + unit * 8;
   }
   char* lds = reinterpret_cast<char*>(smem);
-  auto issue = [&](int c) {
-    char* st = lds + (c % kStages) * kStageBytes;
+  char* bring_lds = lds + kStagesA * kOpStage;
+  auto issue_a = [&](int d) {
+    char* st = lds + (d % kStagesA) * kOpStage;
 #pragma unroll
     for (int i = 0; i < kLoadsPerWave; ++i)
-      __builtin_amdgcn_global_load_lds(src[i] + c * PKC, st + (wave + 8 * i) * kBlkBytes, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(srca[i] + d * DKC, st + (wave + 8 * i) * 1024, 16, 0, 0);
   };
-  // fragment read offset of this lane inside a block: row lr, logical unit kq
-  const uint32_t roff = (uint32_t)(lr * 64 + ((kq ^ ((lr >> 2) & 3)) * 16));
+  // token-row groups past the tile's tokens are not loaded (their LDS rows keep stale data,
+  // which only reaches MFMA output columns that are never stored): nb_loads of the wave's 4
+  const int nb_loads = __builtin_amdgcn_readfirstlane(
+      min(kLoadsPerWave, max(0, ((r1 - r0 + 7) / 8 - wave + 7) / 8)));
+  auto issue_b = [&](int d) {
+    char* st = bring_lds + (d % kStagesB) * kOpStage;
+#pragma unroll
+    for (int i = 0; i < kLoadsPerWave; ++i)
+      if (i < nb_loads)
+        __builtin_amdgcn_global_load_lds(srcb[i] + d * DKC, st + (wave + 8 * i) * 1024, 16, 0, 0);
+  };
+  // fragment read offsets of this lane (row lr of a 16-row block, logical unit s * 4 + kq)
   typedef __attribute__((address_space(3))) char lds_char;
   const uint32_t lds_base = (uint32_t)(uintptr_t)(lds_char*)lds;  // LDS byte address
+  const uint32_t roff0 = (uint32_t)(lr * kRowBytes + ((kq ^ (lr & 7)) * 16));
+  const uint32_t roff1 = (uint32_t)(lr * kRowBytes + (((4 + kq) ^ (lr & 7)) * 16));
 
   f32x4_t acc[4][8];
 #pragma unroll
@@ -217,33 +233,51 @@ __global__ __launch_bounds__(kThreads, 1) void k_prefill_gemm(GemmArgs args) {
   const int nblk = (ntok + 15) >> 4;
   const int nb = __builtin_amdgcn_readfirstlane(min(8, (nblk - wn + 1) >> 1));  // real blocks
 
-  // Software pipeline: the fragments of chunk c + 1 are read from LDS while chunk c is
-  // multiplied; DMA loads run kStages - 2 chunks ahead of the fragment reads.
-  for (int c = 0; c < kStages - 1 && c < nch; ++c) issue(c);
+  // Software pipeline over k-steps j (chunk d = j / 2, half s = j % 2): the fragments of
+  // k-step j + 1 are read while k-step j is multiplied. At the first k-step of chunk d + 1
+  // (after the barrier that makes it visible) the wave issues B(d + 2) then A(d + 3): weight
+  // rows are requested three chunks before use, token rows two. The prologue issues A(0),
+  // B(0), A(1), B(1), A(2) — the order the steps would have — so the loads younger than a
+  // chunk's B load are exactly the next A load.
+  const int nd = op.K / DKC;
+  const int nk = 2 * nd;
+  issue_a(0);
+  if (nd > 0) issue_b(0);
+  if (nd > 1) issue_a(1);
+  if (nd > 1) issue_b(1);
+  if (nd > 2) issue_a(2);
   Frags f0, f1;
-  wait_chunks(min(kStages - 2, nch - 1));
+  // younger than B(0): A(1), B(1), A(2)
+  wait_loads(4 * (nd > 1) + nb_loads * (nd > 1) + 4 * (nd > 2));
   __builtin_amdgcn_s_barrier();
-  read_frags(lds_base + roff, wm, wn, f0);
+  read_frags(lds_base + roff0, lds_base + kStagesA * kOpStage + roff0, wm, wn, f0);
   frags_ready(f0);
-  auto step = [&](int c, Frags& cur, Frags& nxt) {
-    const bool more = c + 1 < nch;
-    MOE_PF_TRACE(0, c);
+  auto step = [&](int j, Frags& cur, Frags& nxt) {
+    const bool more = j + 1 < nk;
+    MOE_PF_TRACE(0, j);
     if (more) {
-      wait_chunks(min(kStages - 3, nch - 2 - c));
-      MOE_PF_TRACE(1, c);
-      __builtin_amdgcn_s_barrier();
-      MOE_PF_TRACE(2, c);
-      if (c + kStages - 1 < nch) issue(c + kStages - 1);
-      read_frags(lds_base + ((c + 1) % kStages) * kStageBytes + roff, wm, wn, nxt);
+      const int jn = j + 1, dn = jn >> 1;
+      if ((jn & 1) == 0) {
+        // chunk dn: younger than B(dn) is A(dn + 1) if it was issued
+        wait_loads(4 * (dn + 1 < nd));
+        MOE_PF_TRACE(1, j);
+        __builtin_amdgcn_s_barrier();
+        MOE_PF_TRACE(2, j);
+        if (dn + kAheadB < nd) issue_b(dn + kAheadB);
+        if (dn + kAheadA < nd) issue_a(dn + kAheadA);
+      }
+      const uint32_t ro = (jn & 1) ? roff1 : roff0;
+      read_frags(lds_base + (dn % kStagesA) * kOpStage + ro,
+                 lds_base + (kStagesA + dn % kStagesB) * kOpStage + ro, wm, wn, nxt);
     }
     mma_frags(cur, nb, acc);
-    MOE_PF_TRACE(3, c);
+    MOE_PF_TRACE(3, j);
     if (more) frags_ready(nxt);
-    MOE_PF_TRACE(4, c);
+    MOE_PF_TRACE(4, j);
   };
-  for (int c = 0; c < nch; c += 2) {
-    step(c, f0, f1);
-    if (c + 1 < nch) step(c + 1, f1, f0);
+  for (int j = 0; j < nk; j += 2) {
+    step(j, f0, f1);
+    step(j + 1, f1, f0);
   }
 
   // ---- epilogue: lane (q = kq, j = lr) holds rows 4q..4q+3 of token column j per block.
@@ -306,7 +340,7 @@ hipError_t launch_prefill_gemm(int mode, const GemmArgs& a_in, int max_tiles, hi
   const int nmax = a.op[0].N > a.op[1].N ? a.op[0].N : a.op[1].N;
   a.nrb = (nmax + out_per_wg - 1) / out_per_wg;
   if (a.nrb <= 0 || max_tiles <= 0) return hipSuccess;
-  const size_t lds = (size_t)kStages * kStageBytes;
+  const size_t lds = (size_t)kLdsBytes;
   a.MTgrid = max_tiles;
   const long long grid = (long long)((max_tiles + kXcds - 1) / kXcds) * kXcds * a.nrb;
   if (mode == kModeSwiglu) {
