@@ -32,24 +32,6 @@ struct GemmOperand {
   int fp8;              // weights are OCP e4m3fn bytes (else bf16)
 };
 
-// Work a launch's last-arriving workgroups do after the GEMM (fused tails).
-struct FuseArgs {
-  int* sync;  // arrival counters (zero on entry; the tail leaves them zero)
-  // route + sort after the router GEMM (the logits are op[1].out, row stride op[1].ld_out)
-  int E, k, bm, has_shared, MT;
-  long long* idx64;
-  int* idx32;
-  uint16_t* w_out;
-  int *counts, *offsets, *order, *table;
-  // combine after the down GEMM: out[t] = combine(y = op[0].out, w, ysh = op[1].out)
-  const uint16_t* w;
-  const uint16_t* seg;
-  long long ld_seg;
-  const uint16_t* residual;
-  uint16_t* out;
-  int round_w, H;
-};
-
 struct GemmArgs {
   GemmOperand op[2];
   const int* table;  // tile table, or null: virtual-expert tiles over rows P .. P + T
@@ -59,14 +41,8 @@ struct GemmArgs {
   int nrb;           // weight-row blocks per tile (set by the launcher)
   int MTgrid;        // tiles the grid covers (set by the launcher)
   int dbg;           // 0; tuning experiments only (MOE_GEMM_DEBUG): 1 skip token-row
-                     // loads, 2 skip MFMAs, 4 skip per-chunk barriers
-  int fuse;          // kFuseNone / kFuseRouteSort / kFuseCombine
-  FuseArgs f;
+                     // loads, 4 skip per-chunk barriers
 };
-
-constexpr int kFuseNone = 0;
-constexpr int kFuseRouteSort = 1;  // router GEMM; the last workgroup routes and sorts
-constexpr int kFuseCombine = 2;    // down GEMM; the last tile of each column block combines
 
 // Launches k_expert_gemm over max_tiles tiles of at most bm (16, 32, 64 or 128) sorted rows.
 // Both operands of one launch must have the same weight type.

@@ -39,7 +39,7 @@
 namespace moe {
 
 // KC: K elements per chunk (128; 32 for small test shapes, bf16 only); R: chunks in flight.
-template <int MODE, int WR, int WK, int TOKB, bool HAS_FP8, int KC, int R = 4, int FUSE = 0>
+template <int MODE, int WR, int WK, int TOKB, bool HAS_FP8, int KC, int R = 4>
 __global__ __launch_bounds__(64 * WR * WK)
 __attribute__((amdgpu_waves_per_eu(TOKB <= 2 && KC >= 64 ? 3 : 1)))
 void k_expert_gemm(GemmArgs args) {
@@ -248,7 +248,7 @@ void k_expert_gemm(GemmArgs args) {
         if (tb < ntb) red[(((wk - 1) * WR + wr) * TOKB + tb) * kWave + lane] = acc[tb];
     }
     __syncthreads();
-    if (FUSE == kFuseNone && wk > 0) return;
+    if (wk > 0) return;
 #pragma unroll
     for (int v = 1; v < WK; ++v)
 #pragma unroll
@@ -300,46 +300,6 @@ void k_expert_gemm(GemmArgs args) {
       *reinterpret_cast<uint2*>(op.out + orow * op.ld_out + n) = pk;
     }
   }
-
-  if (FUSE == kFuseNone) return;
-  // ---- fused tails: the workgroups that arrive last do the dependent step, so it needs no
-  // launch of its own. Writers release their stores before arriving; the last arriver
-  // acquires them. Counters are reset for the next call.
-  __shared__ int last_flag;
-  __threadfence();
-  __syncthreads();
-  if (FUSE == kFuseRouteSort) {
-    if (threadIdx.x == 0) last_flag = atomicAdd(args.f.sync, 1) == (int)gridDim.x - 1;
-    __syncthreads();
-    if (!last_flag) return;
-    __threadfence();
-    const FuseArgs& f = args.f;
-    __shared__ SortLds sl;
-#define MOE_RS(EPL)                                                                           \
-  route_sort_block<EPL>(op.out, op.ld_out, nullptr, nullptr, args.T, f.E, f.k, f.bm,         \
-                        f.has_shared, f.idx64, f.idx32, f.w_out, f.counts, f.offsets, f.order, \
-                        f.table, f.MT, sl)
-    MOE_EPL_DISPATCH(f.E, MOE_RS);
-#undef MOE_RS
-    if (threadIdx.x == 0) *args.f.sync = 0;
-  } else if (FUSE == kFuseCombine) {
-    const int ntiles = args.table[3 * args.MT];
-    int* cnt = args.f.sync + 1 + rb;
-    if (threadIdx.x == 0) last_flag = atomicAdd(cnt, 1) == ntiles - 1;
-    __syncthreads();
-    if (!last_flag) return;
-    __threadfence();
-    const FuseArgs& f = args.f;
-    const int c0 = rb * kOutRowsPerWG;
-    const int ngrp = kOutRowsPerWG / 8;
-    for (int i = threadIdx.x; i < args.T * ngrp; i += blockDim.x) {
-      const int t = i / ngrp;
-      const int c = c0 + (i - t * ngrp) * 8;
-      combine8(args.op[0].out, f.w, args.topk, args.op[1].N > 0 ? args.op[1].out : nullptr,
-               f.seg, f.ld_seg, f.residual, f.out, t, f.H, c, f.round_w);
-    }
-    if (threadIdx.x == 0) *cnt = 0;
-  }
 }
 
 // ------------------------------------------------------------------------ dispatch
@@ -352,19 +312,13 @@ struct Cfg {
 
 template <int MODE, bool HAS_FP8>
 hipError_t launch_cfg(const Cfg& c, const GemmArgs& a, int grid, hipStream_t st) {
-#define MOE_LAUNCH(WR, WK, TOKB, KCV, RV, FU)                                                   \
-  hipLaunchKernelGGL((k_expert_gemm<MODE, WR, WK, TOKB, HAS_FP8, KCV, RV, FU>), dim3(grid),     \
+#define MOE_LAUNCH(WR, WK, TOKB, KCV, RV)                                                       \
+  hipLaunchKernelGGL((k_expert_gemm<MODE, WR, WK, TOKB, HAS_FP8, KCV, RV>), dim3(grid),         \
                      dim3(64 * WR * WK), 0, st, a);                                             \
   return hipGetLastError();
 #define MOE_L(WR, WK, TOKB, KCV, RV)                                                            \
-  if (c.wr == WR && c.wk == WK && c.tokb == TOKB && c.kc == KCV && c.r == RV && a.fuse == 0) { \
-    MOE_LAUNCH(WR, WK, TOKB, KCV, RV, 0)                                                        \
-  }
-// fused-tail variants (PLAIN only): route + sort after the router, combine after down
-#define MOE_LF(WR, WK, TOKB, KCV, RV, FU)                                                       \
-  if (MODE == kModePlain && c.wr == WR && c.wk == WK && c.tokb == TOKB && c.kc == KCV &&       \
-      c.r == RV && a.fuse == FU) {                                                              \
-    MOE_LAUNCH(WR, WK, TOKB, KCV, RV, (MODE == kModePlain ? FU : 0))                            \
+  if (c.wr == WR && c.wk == WK && c.tokb == TOKB && c.kc == KCV && c.r == RV) {                \
+    MOE_LAUNCH(WR, WK, TOKB, KCV, RV)                                                           \
   }
   if constexpr (HAS_FP8) {
     MOE_L(4, 1, 2, 256, 2)
@@ -384,9 +338,6 @@ hipError_t launch_cfg(const Cfg& c, const GemmArgs& a, int grid, hipStream_t st)
     MOE_L(1, 2, 1, 128, 4)
     MOE_L(1, 1, 1, 128, 4)
     MOE_L(4, 1, 8, 64, 4)
-    MOE_LF(1, 4, 1, 64, 8, kFuseCombine)
-    MOE_LF(2, 1, 2, 64, 8, kFuseCombine)
-    MOE_LF(4, 1, 4, 64, 8, kFuseCombine)
   } else {
     MOE_L(1, 8, 1, 64, 4)
     MOE_L(1, 4, 1, 64, 4)
@@ -403,17 +354,8 @@ hipError_t launch_cfg(const Cfg& c, const GemmArgs& a, int grid, hipStream_t st)
     MOE_L(1, 1, 1, 32, 4)
     MOE_L(1, 1, 2, 32, 4)
     MOE_L(1, 1, 4, 32, 4)
-    MOE_LF(1, 4, 1, 64, 4, kFuseRouteSort)
-    MOE_LF(1, 1, 1, 32, 4, kFuseRouteSort)
-    MOE_LF(1, 4, 1, 64, 4, kFuseCombine)
-    MOE_LF(2, 1, 2, 64, 4, kFuseCombine)
-    MOE_LF(4, 1, 4, 64, 4, kFuseCombine)
-    MOE_LF(1, 1, 1, 32, 4, kFuseCombine)
-    MOE_LF(1, 1, 2, 32, 4, kFuseCombine)
-    MOE_LF(1, 1, 4, 32, 4, kFuseCombine)
   }
 #undef MOE_L
-#undef MOE_LF
 #undef MOE_LAUNCH
   return hipErrorInvalidConfiguration;
 }
@@ -490,8 +432,6 @@ hipError_t launch_expert_gemm(int mode, int role, int bm, const GemmArgs& a_in, 
   for (int i = 0; i < n; ++i) {
     const Cfg& c = prefs[i];
     if (!fits(c, mode, a.op[0]) || !fits(c, mode, a.op[1])) continue;
-    // the fused route + sort runs in one workgroup: one thread per expert at least
-    if (a.fuse == kFuseRouteSort && 64 * c.wr * c.wk < a.f.E) continue;
     if (c.wk * 2 * c.tokb * 16 * (c.kc / 8 + (c.kc == 64 ? 2 : 1)) * 16 > 65536) continue;
     int rows = (mode == kModeSwiglu ? 8 : 16) * c.wr;
     int nmax = a.op[0].N > a.op[1].N ? a.op[0].N : a.op[1].N;

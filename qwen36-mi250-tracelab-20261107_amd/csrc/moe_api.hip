@@ -84,18 +84,9 @@ bool decode_enabled() {
 
 size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
 
-// The first kSyncBytes of every workspace hold the fused tails' arrival counters: zero
-// before the first call, and every call leaves them zero.
+// The first kSyncBytes of every workspace are reserved for cross-workgroup counters: zero
+// before the first call, and every call leaves them zero (no current kernel uses them).
 constexpr size_t kSyncBytes = 4096;
-
-// Which fused tails are on: MOE_FUSE = "route", "combine", "route,combine" or "none"
-// (tuning knob, read per call). Default: none (measured: no gain at decode batch 1, a
-// loss at batch 64 for route; the combine tail's release fences cost far more than a launch).
-bool fuse_enabled(const char* what) {
-  const char* env = getenv("MOE_FUSE");
-  if (!env) return false;
-  return strstr(env, what) != nullptr;
-}
 
 // Sequential carve of a caller-provided workspace.
 struct Carver {
@@ -266,13 +257,10 @@ int run_gate_up(const void* x, int T, int H, int E, int k, int I, const void* ga
   return hip_check(err, "gate_up launch");
 }
 
-// With fuse (a FuseArgs for the combine), the launch also combines: the last tile of each
-// column block writes those columns of out. Returns MOE_EINVAL-free status 1 through
-// *fused = false when that launch shape cannot fuse (the caller combines separately).
 int run_down(const void* act, int T, int H, int E, int k, int I, const void* down,
              const float* dn_scale, int wdtype, const void* sh_down, int IS, const void* act_sh,
              const int* order, const int* table, int MT, int bm, void* y, void* y_sh,
-             hipStream_t s, const FuseArgs* fuse = nullptr, bool* fused = nullptr) {
+             hipStream_t s) {
   GemmArgs a{};
   a.op[0] = down_operand(down, dn_scale, H, I, act, y);
   a.op[0].fp8 = wdtype == MOE_WEIGHTS_FP8_E4M3;
@@ -297,20 +285,6 @@ int run_down(const void* act, int T, int H, int E, int k, int I, const void* dow
   a.P = T * k;
   a.E = E;
   a.T = T;
-  if (fused) *fused = false;
-  const bool split = a.op[1].N > 0 && a.op[0].fp8 != a.op[1].fp8;
-  if (fuse && fused && fuse_enabled("combine") && bm != prefill_tile_rows() && !split &&
-      H / 16 < (int)(kSyncBytes / 4) - 1) {
-    GemmArgs f = a;
-    f.fuse = kFuseCombine;
-    f.f = *fuse;
-    hipError_t err = launch_expert_gemm(kModePlain, kRoleDown, bm, f, MT, s);
-    if (err == hipSuccess) {
-      *fused = true;
-      return MOE_OK;
-    }
-    if (err != hipErrorInvalidValue) return hip_check(err, "down+combine launch");
-  }
   hipError_t err = bm == prefill_tile_rows() ? launch_prefill_gemm(kModePlain, a, MT, s)
                                              : launch_split(kModePlain, kRoleDown, bm, a, MT, s);
   if (err == hipErrorInvalidValue)
@@ -336,9 +310,9 @@ int moe_max_tiles(int T, int k, int E, int bm, int has_shared) {
 }  // extern "C"
 
 namespace {
-// Router GEMM; with fa, its last workgroup also routes and sorts (decode-sized batches).
+// Router GEMM (PLAIN, identity tiles over the tokens).
 hipError_t launch_router(const void* x, int T, int H, const void* w_pack, int n_pack,
-                         void* logits, hipStream_t st, const FuseArgs* fa) {
+                         void* logits, hipStream_t st) {
   GemmArgs a{};
   GemmOperand& v = a.op[1];
   v.w = w_pack;
@@ -355,16 +329,12 @@ hipError_t launch_router(const void* x, int T, int H, const void* w_pack, int n_
   a.P = 0;
   a.E = 0;
   a.T = T;
-  if (fa) {
-    a.fuse = kFuseRouteSort;
-    a.f = *fa;
-  }
   // Token rows per tile: 16-token tiles (K split over 8 waves) give the most waves for a
   // handful of tokens; larger batches re-read the 1 MiB weight once per tile, so their
   // tiles grow with T (measured: 16 up to 64 tokens, 32 up to 1024, 64 above).
   int bm = T <= 64 ? 16 : (T <= 1024 ? 32 : 64);
   if (const char* env = getenv("MOE_ROUTER_BM")) bm = atoi(env);
-  if (bm == prefill_tile_rows() && !fa) {
+  if (bm == prefill_tile_rows()) {
     hipError_t err = launch_prefill_gemm(kModePlain, a, (T + bm - 1) / bm, st);
     if (err != hipErrorInvalidValue) return err;
     bm = 16;
@@ -383,7 +353,7 @@ int moe_router_logits(const void* x, int T, int H, const void* w_pack, int n_pac
             n_pack);
   CHECK_ARG(x && w_pack && logits, "null pointer");
   if (T == 0) return MOE_OK;
-  hipError_t err = launch_router(x, T, H, w_pack, n_pack, logits, (hipStream_t)stream, nullptr);
+  hipError_t err = launch_router(x, T, H, w_pack, n_pack, logits, (hipStream_t)stream);
   if (err == hipErrorInvalidValue) return fail(MOE_EINVAL, "router: no configuration for H=%d", H);
   return hip_check(err, "router launch");
 }
@@ -634,16 +604,9 @@ int moe_experts_forward(const void* x, int T, int H, int E, int k, int I,
   rc = run_gate_up(x, T, H, E, k, I, gate_up, gu_scale, wdtype, nullptr, nullptr, 0, w.order,
                    w.table, w.MT, w.bm, w.act, nullptr, s);
   if (rc) return rc;
-  FuseArgs fa{};
-  fa.sync = w.sync;
-  fa.w = static_cast<const uint16_t*>(top_k_weights);
-  fa.out = static_cast<uint16_t*>(out);
-  fa.round_w = mode == MOE_ROUND_PRODUCT;
-  fa.H = H;
-  bool fused = false;
   rc = run_down(w.act, T, H, E, k, I, down, dn_scale, wdtype, nullptr, 0, nullptr, w.order, w.table,
-                w.MT, w.bm, w.y, nullptr, s, &fa, &fused);
-  if (rc || fused) return rc;
+                w.MT, w.bm, w.y, nullptr, s);
+  if (rc) return rc;
   return hip_check(launch_combine(w.y, static_cast<const uint16_t*>(top_k_weights), k, nullptr,
                                   nullptr, 0, nullptr, static_cast<uint16_t*>(out), T, H,
                                   mode == MOE_ROUND_PRODUCT, s),
@@ -747,51 +710,17 @@ int moe_block_forward(const void* x, int T, int H, int E, int k, int I, int IS,
       return hip_check(launch_decode_down(d, s), "decode down launch");
     }
   }
-  bool routed_in_router = false;
-  if (fuse_enabled("route") && sort_uses_small(T * k, E)) {
-    FuseArgs fa{};
-    fa.sync = w.sync;
-    fa.E = E;
-    fa.k = k;
-    fa.bm = w.bm;
-    fa.has_shared = 1;
-    fa.MT = w.MT;
-    fa.idx64 = i64;
-    fa.idx32 = w.idx32;
-    fa.w_out = wt;
-    fa.counts = w.counts;
-    fa.offsets = w.offsets;
-    fa.order = w.order;
-    fa.table = w.table;
-    hipError_t err = launch_router(x, T, H, w_pack, n_pack, lg, s, &fa);
-    if (err == hipSuccess)
-      routed_in_router = true;
-    else if (err != hipErrorInvalidValue)
-      return hip_check(err, "router+route launch");
-  }
-  if (!routed_in_router) {
-    rc = moe_router_logits(x, T, H, w_pack, n_pack, lg, stream);
-    if (rc) return rc;
-    HIP_TRY(launch_route_sort(lg, n_pack, nullptr, nullptr, T, E, k, w.bm, 1, i64, w.idx32, wt,
-                              w.counts, w.offsets, w.order, w.table, w.MT, w.scratch, s),
-            "route/sort launch");
-  }
+  rc = moe_router_logits(x, T, H, w_pack, n_pack, lg, stream);
+  if (rc) return rc;
+  HIP_TRY(launch_route_sort(lg, n_pack, nullptr, nullptr, T, E, k, w.bm, 1, i64, w.idx32, wt,
+                            w.counts, w.offsets, w.order, w.table, w.MT, w.scratch, s),
+          "route/sort launch");
   rc = run_gate_up(x, T, H, E, k, I, gate_up, gu_scale, wdtype, sh_gate, sh_up, IS, w.order,
                    w.table, w.MT, w.bm, w.act, w.act_sh, s);
   if (rc) return rc;
-  FuseArgs fc{};
-  fc.sync = w.sync;
-  fc.w = wt;
-  fc.seg = lg + E;
-  fc.ld_seg = n_pack;
-  fc.residual = static_cast<const uint16_t*>(residual);
-  fc.out = static_cast<uint16_t*>(out);
-  fc.round_w = mode == MOE_ROUND_PRODUCT;
-  fc.H = H;
-  bool fused = false;
   rc = run_down(w.act, T, H, E, k, I, down, dn_scale, wdtype, sh_down, IS, w.act_sh, w.order,
-                w.table, w.MT, w.bm, w.y, w.y_sh, s, &fc, &fused);
-  if (rc || fused) return rc;
+                w.table, w.MT, w.bm, w.y, w.y_sh, s);
+  if (rc) return rc;
   return hip_check(launch_combine(w.y, wt, k, w.y_sh, lg + E, n_pack,
                                   static_cast<const uint16_t*>(residual),
                                   static_cast<uint16_t*>(out), T, H, mode == MOE_ROUND_PRODUCT, s),

@@ -1,6 +1,6 @@
 // Device-side routing (softmax / top-k) and sort helpers shared by the standalone
-// route / sort kernels (route_sort.hip) and the router GEMM's fused routing tail
-// (expert_gemm.hip). See route_sort.hip for the contract.
+// route / sort kernels (route_sort.hip) and the decode gate_up kernel (decode.hip). See
+// route_sort.hip for the contract.
 #pragma once
 #include "moe_common.h"
 

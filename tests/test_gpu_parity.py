@@ -343,9 +343,9 @@ def test_block_residual(pkg, dev):
     assert torch.equal(b.cpu(), want)
 
 
-def test_fused_tails_leave_sync_area_zero(pkg, dev, full_layer):
-    """The fused route/sort and combine tails reset their arrival counters: after calls of
-    every regime the workspace head is zero again, and repeated calls give the same bits."""
+def test_calls_leave_sync_area_zero_and_repeat(pkg, dev, full_layer):
+    """After calls of every regime (decode path, tiled decode, mid-size, multi-block sort)
+    the reserved workspace head is still zero, and repeated calls give the same bits."""
     w, _ = full_layer
     mlp = _gpu_mlp(w, dev)
     g = torch.Generator().manual_seed(5)
