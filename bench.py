@@ -250,12 +250,26 @@ def cpu_baseline(torch, seconds):
         n += 1
     times.sort()
     med = times[len(times) // 2]
+    others = {}
+    for name, T in (("c3", 64), ("c4", 4096)):
+        # the same CPU path at the other batch sizes, a few calls each (bounded sample;
+        # C3 with plain random routing, C5 is C3-like at 32 tokens with bf16 weights)
+        xb = torch.randn(T, H, generator=g).to(torch.bfloat16)
+        orc.block_bf16(xb, w, K_TOP)
+        ts, tb = [], time.perf_counter()
+        while len(ts) < 3 or (time.perf_counter() - tb < seconds / 3 and len(ts) < 50):
+            t1 = time.perf_counter()
+            orc.block_bf16(xb, w, K_TOP)
+            ts.append(time.perf_counter() - t1)
+        ts.sort()
+        others[name] = {"T": T, "us_per_layer": round(ts[len(ts) // 2] * 1e6, 1), "calls": len(ts)}
     return {
         "value": round(med * 1e6, 1), "unit": "us/layer", "cores": torch.get_num_threads(),
         "affinity_cores": len(os.sched_getaffinity(0)), "kind": "port",
         "sample": f"C2 decode batch 1, {n} layer calls of the bf16 CPU torch path "
                   f"(oracle.block_bf16 = Transformers block + batched_mm experts) over "
                   f"{seconds:.0f}s, median",
+        "other_batches": others,
     }
 
 
