@@ -84,6 +84,12 @@ bool decode_enabled() {
   return !(env && env[0] == '0');
 }
 
+// Prefill shared-expert tiles on the auxiliary stream unless MOE_PREFILL_SIDE=0.
+bool prefill_side_enabled() {
+  const char* env = getenv("MOE_PREFILL_SIDE");
+  return !(env && env[0] == '0');
+}
+
 size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
 
 // The first kSyncBytes of every workspace are reserved for cross-workgroup counters: zero
@@ -194,6 +200,30 @@ AuxStream* aux_stream(hipStream_t caller) {
   return &a;
 }
 
+// Prefill tiles: the routed tiles fill whole rounds of one workgroup per CU (256 experts x
+// 4 or 8 row blocks), and the shared expert's tiles would add a last, mostly idle round; run
+// them as a second launch on the auxiliary stream instead, where they fill the gaps of the
+// routed launch.
+hipError_t launch_prefill_split(int mode, const GemmArgs& a, int MT, hipStream_t s) {
+  AuxStream* aux = a.op[0].N > 0 && a.op[1].N > 0 && a.table ? aux_stream(s) : nullptr;
+  if (!aux || !prefill_side_enabled()) return launch_prefill_gemm(mode, a, MT, s);
+  GemmArgs v = a;  // no table: the prefill kernel reads tile i as shared rows [256 i, 256 i + 256)
+  v.op[0].N = 0;
+  v.table = nullptr;
+  hipError_t e = hipEventRecord(aux->fork, s);
+  if (e == hipSuccess) e = hipStreamWaitEvent(aux->s, aux->fork, 0);
+  if (e != hipSuccess) return e;
+  e = launch_prefill_gemm(mode, v, (a.T + prefill_tile_rows() - 1) / prefill_tile_rows(), aux->s);
+  if (e != hipSuccess) return e;
+  GemmArgs r = a;
+  r.op[1].N = 0;
+  e = launch_prefill_gemm(mode, r, MT, s);
+  if (e != hipSuccess) return e;
+  e = hipEventRecord(aux->join, aux->s);
+  if (e == hipSuccess) e = hipStreamWaitEvent(s, aux->join, 0);
+  return e;
+}
+
 // A launch whose routed experts are fp8 and shared expert bf16 runs as two launches (each
 // kernel is compiled for one weight type); the shared one goes to the auxiliary stream so
 // the two overlap.
@@ -252,7 +282,7 @@ int run_gate_up(const void* x, int T, int H, int E, int k, int I, const void* ga
   a.P = T * k;
   a.E = E;
   a.T = T;
-  hipError_t err = bm == prefill_tile_rows() ? launch_prefill_gemm(kModeSwiglu, a, MT, s)
+  hipError_t err = bm == prefill_tile_rows() ? launch_prefill_split(kModeSwiglu, a, MT, s)
                                              : launch_split(kModeSwiglu, kRoleGateUp, bm, a, MT, s);
   if (err == hipErrorInvalidValue)
     return fail(MOE_EINVAL, "gate_up: no kernel configuration for H=%d I=%d IS=%d", H, I, IS);
@@ -287,7 +317,7 @@ int run_down(const void* act, int T, int H, int E, int k, int I, const void* dow
   a.P = T * k;
   a.E = E;
   a.T = T;
-  hipError_t err = bm == prefill_tile_rows() ? launch_prefill_gemm(kModePlain, a, MT, s)
+  hipError_t err = bm == prefill_tile_rows() ? launch_prefill_split(kModePlain, a, MT, s)
                                              : launch_split(kModePlain, kRoleDown, bm, a, MT, s);
   if (err == hipErrorInvalidValue)
     return fail(MOE_EINVAL, "down: no kernel configuration for H=%d I=%d IS=%d", H, I, IS);
