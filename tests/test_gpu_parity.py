@@ -329,6 +329,29 @@ def test_block_full_shape_prefill(pkg, dev, full_layer, T):
     assert torch.isfinite(out.float()).all()
 
 
+@pytest.mark.parametrize("T", [1, 64, 1024])
+def test_shared_up_below_gate(pkg, dev, full_layer, T):
+    """The shared expert's gate and up projections are separate tensors at any distance and
+    in either order in memory: here up sits just below gate (a negative gate -> up offset)
+    in every regime (decode, expert GEMM, prefill tiles). Same outputs as with the tensors
+    in the usual order."""
+    _say("shared up below gate", T)
+    w, _ = full_layer
+    g = torch.Generator().manual_seed(50 + T)
+    x = torch.randn(T, 2048, generator=g).to(BF16).to(dev)
+    mlp = _gpu_mlp(w, dev)
+    both = torch.empty((2,) + tuple(w["sh_gate"].shape), dtype=BF16, device=dev)
+    both[0].copy_(w["sh_up"])
+    both[1].copy_(w["sh_gate"])
+    mlp2 = _gpu_mlp(w, dev)
+    mlp2.shared_expert.gate_proj.weight = both[1]
+    mlp2.shared_expert.up_proj.weight = both[0]
+    a = pkg.block.moe(x, mlp, 8)
+    b = pkg.block.moe(x, mlp2, 8)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+
+
 def test_block_residual(pkg, dev):
     H, E, K, I = 256, 16, 4, 128
     w = orc.make_weights(H, E, I, I, seed=1)
