@@ -90,6 +90,16 @@ bool prefill_side_enabled() {
   return !(env && env[0] == '0');
 }
 
+// Block forward: the shared expert on the auxiliary stream (MOE_BLOCK_SIDE=0 / 1 forces it
+// off / on; by default where it runs as separate launches anyway: fp8 routed experts or
+// prefill tiles).
+bool block_side_enabled(int T, bool fp8, int bm) {
+  const char* env = getenv("MOE_BLOCK_SIDE");
+  if (env) return env[0] == '1';
+  (void)T;
+  return fp8 || bm == 256;
+}
+
 size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
 
 // The first kSyncBytes of every workspace are reserved for cross-workgroup counters: zero
@@ -253,10 +263,38 @@ hipError_t launch_split(int mode, int role, int bm, const GemmArgs& a, int MT, h
   return err;
 }
 
+// Which projections a grouped launch runs: both weight families (split as above when
+// needed), the routed experts only, or the shared expert only (its tiles from the token
+// count alone).
+enum Part { kBoth = 0, kRoutedOnly = 1, kSharedOnly = 2 };
+
+hipError_t launch_part(int mode, int role, int bm, const GemmArgs& a, int MT, int part,
+                       hipStream_t s) {
+  const bool prefill = bm == prefill_tile_rows();
+  if (part == kRoutedOnly) {
+    GemmArgs r = a;
+    r.op[1].N = 0;
+    return prefill ? launch_prefill_gemm(mode, r, MT, s) : launch_expert_gemm(mode, role, bm, r, MT, s);
+  }
+  if (part == kSharedOnly) {
+    GemmArgs v = a;
+    v.table = nullptr;
+    const int tiles = (a.T + bm - 1) / bm;
+    if (prefill) {
+      v.op[0].N = 0;  // the prefill kernel reads tile i as shared rows [bm i, bm i + bm)
+      return launch_prefill_gemm(mode, v, tiles, s);
+    }
+    v.op[0] = v.op[1];  // the configuration follows op[0]'s weight type
+    v.op[0].N = 0;
+    return launch_expert_gemm(mode, role, bm, v, tiles, s);
+  }
+  return prefill ? launch_prefill_split(mode, a, MT, s) : launch_split(mode, role, bm, a, MT, s);
+}
+
 int run_gate_up(const void* x, int T, int H, int E, int k, int I, const void* gate_up,
                 const float* gu_scale, int wdtype, const void* sh_gate, const void* sh_up, int IS,
                 const int* order, const int* table, int MT, int bm, void* act, void* act_sh,
-                hipStream_t s) {
+                hipStream_t s, int part = kBoth) {
   GemmArgs a{};
   a.op[0] = gate_up_operand(gate_up, gu_scale, H, I, x, act);
   a.op[0].fp8 = wdtype == MOE_WEIGHTS_FP8_E4M3;
@@ -282,8 +320,7 @@ int run_gate_up(const void* x, int T, int H, int E, int k, int I, const void* ga
   a.P = T * k;
   a.E = E;
   a.T = T;
-  hipError_t err = bm == prefill_tile_rows() ? launch_prefill_split(kModeSwiglu, a, MT, s)
-                                             : launch_split(kModeSwiglu, kRoleGateUp, bm, a, MT, s);
+  hipError_t err = launch_part(kModeSwiglu, kRoleGateUp, bm, a, MT, sh_gate ? part : kBoth, s);
   if (err == hipErrorInvalidValue)
     return fail(MOE_EINVAL, "gate_up: no kernel configuration for H=%d I=%d IS=%d", H, I, IS);
   return hip_check(err, "gate_up launch");
@@ -292,7 +329,7 @@ int run_gate_up(const void* x, int T, int H, int E, int k, int I, const void* ga
 int run_down(const void* act, int T, int H, int E, int k, int I, const void* down,
              const float* dn_scale, int wdtype, const void* sh_down, int IS, const void* act_sh,
              const int* order, const int* table, int MT, int bm, void* y, void* y_sh,
-             hipStream_t s) {
+             hipStream_t s, int part = kBoth) {
   GemmArgs a{};
   a.op[0] = down_operand(down, dn_scale, H, I, act, y);
   a.op[0].fp8 = wdtype == MOE_WEIGHTS_FP8_E4M3;
@@ -317,8 +354,7 @@ int run_down(const void* act, int T, int H, int E, int k, int I, const void* dow
   a.P = T * k;
   a.E = E;
   a.T = T;
-  hipError_t err = bm == prefill_tile_rows() ? launch_prefill_split(kModePlain, a, MT, s)
-                                             : launch_split(kModePlain, kRoleDown, bm, a, MT, s);
+  hipError_t err = launch_part(kModePlain, kRoleDown, bm, a, MT, sh_down ? part : kBoth, s);
   if (err == hipErrorInvalidValue)
     return fail(MOE_EINVAL, "down: no kernel configuration for H=%d I=%d IS=%d", H, I, IS);
   return hip_check(err, "down launch");
@@ -752,17 +788,38 @@ int moe_block_forward(const void* x, int T, int H, int E, int k, int I, int IS,
       return hip_check(launch_decode_down(d, s), "decode down launch");
     }
   }
+  // The shared expert depends on x alone: where its projections would run as launches of
+  // their own anyway (fp8 routed experts, prefill tiles), they run on the auxiliary stream
+  // from the start of the block, beside the router and routing, and join before the combine.
+  AuxStream* aux = block_side_enabled(T, wdtype == MOE_WEIGHTS_FP8_E4M3, w.bm) ? aux_stream(s)
+                                                                               : nullptr;
+  const int part = aux ? kRoutedOnly : kBoth;
+  if (aux) {
+    HIP_TRY(hipEventRecord(aux->fork, s), "fork");
+    HIP_TRY(hipStreamWaitEvent(aux->s, aux->fork, 0), "fork");
+    rc = run_gate_up(x, T, H, E, k, I, gate_up, gu_scale, wdtype, sh_gate, sh_up, IS, w.order,
+                     w.table, w.MT, w.bm, w.act, w.act_sh, aux->s, kSharedOnly);
+    if (rc) return rc;
+    rc = run_down(w.act, T, H, E, k, I, down, dn_scale, wdtype, sh_down, IS, w.act_sh, w.order,
+                  w.table, w.MT, w.bm, w.y, w.y_sh, aux->s, kSharedOnly);
+    if (rc) return rc;
+  }
   rc = moe_router_logits(x, T, H, w_pack, n_pack, lg, stream);
   if (rc) return rc;
-  HIP_TRY(launch_route_sort(lg, n_pack, nullptr, nullptr, T, E, k, w.bm, 1, i64, w.idx32, wt,
-                            w.counts, w.offsets, w.order, w.table, w.MT, w.scratch, s),
+  HIP_TRY(launch_route_sort(lg, n_pack, nullptr, nullptr, T, E, k, w.bm, aux ? 0 : 1, i64,
+                            w.idx32, wt, w.counts, w.offsets, w.order, w.table, w.MT, w.scratch,
+                            s),
           "route/sort launch");
   rc = run_gate_up(x, T, H, E, k, I, gate_up, gu_scale, wdtype, sh_gate, sh_up, IS, w.order,
-                   w.table, w.MT, w.bm, w.act, w.act_sh, s);
+                   w.table, w.MT, w.bm, w.act, w.act_sh, s, part);
   if (rc) return rc;
   rc = run_down(w.act, T, H, E, k, I, down, dn_scale, wdtype, sh_down, IS, w.act_sh, w.order,
-                w.table, w.MT, w.bm, w.y, w.y_sh, s);
+                w.table, w.MT, w.bm, w.y, w.y_sh, s, part);
   if (rc) return rc;
+  if (aux) {
+    HIP_TRY(hipEventRecord(aux->join, aux->s), "join");
+    HIP_TRY(hipStreamWaitEvent(s, aux->join, 0), "join");
+  }
   return hip_check(launch_combine(w.y, wt, k, w.y_sh, lg + E, n_pack,
                                   static_cast<const uint16_t*>(residual),
                                   static_cast<uint16_t*>(out), T, H, mode == MOE_ROUND_PRODUCT, s),
