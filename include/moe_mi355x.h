@@ -53,8 +53,9 @@ int moe_abi_version(void);
 const char* moe_last_error(void);
 
 /* Sorted rows per tile (bm) the fused entry points use for T tokens: 16 up to 16 tokens,
- * 32 up to 512, 64 above. A table passed to moe_grouped_gate_up / moe_grouped_down must be
- * built with a bm of 16, 32, 64 or 128. */
+ * 32 up to 512, above that 256 (the prefill tiles: bf16 weights, hidden a multiple of 256,
+ * intermediates of 128) or else 64. A table passed to moe_grouped_gate_up /
+ * moe_grouped_down must be built with a bm of 16, 32, 64, 128 or 256. */
 int moe_tile_rows(int T);
 
 /* Tile-table capacity for T tokens: ceil(T*k/bm) + min(E, T*k) (+ ceil(T/bm) shared tiles). */

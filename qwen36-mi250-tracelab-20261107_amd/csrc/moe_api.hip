@@ -41,13 +41,13 @@ int tile_rows_for(int T, bool fp8 = false, int H = 2048, int I = 512, int IS = 5
   const char* env = getenv("MOE_TILE_ROWS");
   if (env) {
     int v = atoi(env);
-    if (v == 16 || v == 32 || v == 64 || v == 128 || v == 256) return v;
+    if (v == 16 || v == 32 || v == 64 || v == 128 || v == prefill_tile_rows()) return v;
   }
   if (T <= 16) return 16;
   if (T <= 512) return 32;
   const bool prefill_ok = !fp8 && H % 256 == 0 && I % 128 == 0 && IS % 128 == 0 &&
                           H % 64 == 0 && I % 64 == 0 && IS % 64 == 0;
-  return prefill_ok ? 256 : 64;
+  return prefill_ok ? prefill_tile_rows() : 64;
 }
 
 thread_local std::string g_err;
@@ -97,7 +97,7 @@ bool block_side_enabled(int T, bool fp8, int bm) {
   const char* env = getenv("MOE_BLOCK_SIDE");
   if (env) return env[0] == '1';
   (void)T;
-  return fp8 || bm == 256;
+  return fp8 || bm == prefill_tile_rows();
 }
 
 size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
@@ -210,14 +210,14 @@ AuxStream* aux_stream(hipStream_t caller) {
   return &a;
 }
 
-// Prefill tiles: the routed tiles fill whole rounds of one workgroup per CU (256 experts x
+// Prefill tiles: the routed tiles fill whole rounds of one workgroup per CU (~256 experts x
 // 4 or 8 row blocks), and the shared expert's tiles would add a last, mostly idle round; run
 // them as a second launch on the auxiliary stream instead, where they fill the gaps of the
 // routed launch.
 hipError_t launch_prefill_split(int mode, const GemmArgs& a, int MT, hipStream_t s) {
   AuxStream* aux = a.op[0].N > 0 && a.op[1].N > 0 && a.table ? aux_stream(s) : nullptr;
   if (!aux || !prefill_side_enabled()) return launch_prefill_gemm(mode, a, MT, s);
-  GemmArgs v = a;  // no table: the prefill kernel reads tile i as shared rows [256 i, 256 i + 256)
+  GemmArgs v = a;  // no table: the prefill kernel reads tile i as shared rows [bm i, bm i + bm)
   v.op[0].N = 0;
   v.table = nullptr;
   hipError_t e = hipEventRecord(aux->fork, s);
@@ -477,8 +477,8 @@ int moe_grouped_gate_up(const void* x, int T, int H, int E, int k, int I, const 
                          (((intptr_t)sh_up - (intptr_t)sh_gate) & 1) == 0),
             "shared expert needs sh_up, act_sh and IS a multiple of 32");
   if (T == 0) return MOE_OK;
-  CHECK_ARG(bm == 16 || bm == 32 || bm == 64 || bm == 128 || bm == 256,
-            "bm must be 16, 32, 64, 128 or 256 (got %d)", bm);
+  CHECK_ARG(bm == 16 || bm == 32 || bm == 64 || bm == 128 || bm == prefill_tile_rows(),
+            "bm must be 16, 32, 64, 128 or %d (got %d)", prefill_tile_rows(), bm);
   return run_gate_up(x, T, H, E, k, I, gate_up, gu_scale, wdtype, sh_gate, sh_up, IS, order,
                      table, max_tiles, bm, act, act_sh, (hipStream_t)stream);
 }
@@ -495,8 +495,8 @@ int moe_grouped_down(const void* act, int T, int H, int E, int k, int I, const v
   CHECK_ARG(!sh_down || (act_sh && y_sh && IS >= 32 && IS % 32 == 0),
             "shared expert needs act_sh, y_sh and IS a multiple of 32");
   if (T == 0) return MOE_OK;
-  CHECK_ARG(bm == 16 || bm == 32 || bm == 64 || bm == 128 || bm == 256,
-            "bm must be 16, 32, 64, 128 or 256 (got %d)", bm);
+  CHECK_ARG(bm == 16 || bm == 32 || bm == 64 || bm == 128 || bm == prefill_tile_rows(),
+            "bm must be 16, 32, 64, 128 or %d (got %d)", prefill_tile_rows(), bm);
   return run_down(act, T, H, E, k, I, down, dn_scale, wdtype, sh_down, IS, act_sh, order, table,
                   max_tiles, bm, y, y_sh, (hipStream_t)stream);
 }

@@ -146,7 +146,9 @@ __global__ __launch_bounds__(kThreads, 1) void k_prefill_gemm(GemmArgs args) {
     if (tile >= args.table[3 * args.MT]) return;
     e = args.table[tile];
     r0 = args.table[args.MT + tile];
-    r1 = args.table[2 * args.MT + tile];
+    // the table holds the expert's end row; this tile is its next PBM rows at most (the
+    // token-row ring stages hold PBM rows)
+    r1 = min(args.table[2 * args.MT + tile], r0 + PBM);
   } else {
     e = args.E;
     r0 = args.P + tile * PBM;
