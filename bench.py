@@ -100,16 +100,15 @@ def layer_bytes(D, T, fp8=False):
     return weights + acts
 
 
-def gate_up_bytes(D, T, fp8=False, shared=True):
+def gate_up_bytes(D, T, fp8=False, logits=False):
     """Algorithmic bytes of one gate_up launch: each distinct expert's gate/up rows once
-    (+ fp32 row scales), the token rows, the activations written; with ``shared`` the
-    shared expert's rows and activations (grouped launch), without it the router logits
-    the decode launch routes from."""
+    (+ fp32 row scales), the shared expert's gate/up rows, the token rows, the activations
+    written; with ``logits`` also the router logits the decode launch routes from."""
     per_expert = 2 * I * H * (1 if fp8 else 2) + (2 * I * 4 if fp8 else 0)
-    b = D * per_expert + T * H * 2 + T * K_TOP * I * 2
-    if shared:
-        return b + 2 * IS * H * 2 + T * IS * 2
-    return b + T * 320 * 2  # logits rows [T, n_pack = 320]
+    b = D * per_expert + 2 * IS * H * 2 + T * H * 2 + T * K_TOP * I * 2 + T * IS * 2
+    if logits:
+        b += T * 320 * 2  # logits rows [T, n_pack = 320]
+    return b
 
 
 def capture(torch, fn):
@@ -192,8 +191,8 @@ def run_config(torch, dev, name, T, layers, steps, warmup, zipf=False, fp8=False
     del graph
 
     # the dominant kernel alone, as the block launches it: the decode gate_up (routing in the
-    # launch, routed experts) for decode-path shapes, else the grouped gate_up (routed +
-    # shared) over the sorted tile table
+    # launch, routed experts + the shared expert's gate/up rows) for decode-path shapes, else
+    # the grouped gate_up (routed + shared) over the sorted tile table
     decode = pkg.ops.decode_fits(T, H, E, K_TOP, I, IS)
     sps = []
     for mlp, x in zip(mlps, xs):
@@ -211,7 +210,9 @@ def run_config(torch, dev, name, T, layers, steps, warmup, zipf=False, fp8=False
             scale = getattr(ex, "gate_up_scale", None)
             if decode:
                 pkg.ops.decode_gate_up(x, ex.gate_up_proj, K_TOP, logits=sp, experts=E,
-                                       scale=scale)
+                                       scale=scale,
+                                       shared=(mlp.shared_expert.gate_proj.weight,
+                                               mlp.shared_expert.up_proj.weight))
             else:
                 pkg.ops.grouped_gate_up(x, K_TOP, ex.gate_up_proj, sp, scale=scale,
                                         shared=(mlp.shared_expert.gate_proj.weight,
@@ -220,7 +221,7 @@ def run_config(torch, dev, name, T, layers, steps, warmup, zipf=False, fp8=False
     graph = capture(torch, gate_up_pass)
     ms = time_graph(torch, graph, reps, wreps)
     us_k = ms * 1000.0 / nsteps
-    kbytes = sum(gate_up_bytes(d, T, fp8, shared=not decode) for d in Ds) / len(Ds)
+    kbytes = sum(gate_up_bytes(d, T, fp8, logits=decode) for d in Ds) / len(Ds)
     res["gate_up_kernel"] = "k_dec_gate_up" if decode else (
         "k_prefill_gemm" if T > 512 and not fp8 else "k_expert_gemm")
     res["gate_up_us"] = round(us_k, 3)

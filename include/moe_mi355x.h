@@ -135,12 +135,15 @@ int moe_decode_router(const void* x, int T, int H, const void* w_pack, int n_pac
 /* Stage 2: act [T*k, I] = SwiGLU of the routed experts. With logits (first E columns, row
  * stride n_pack) the softmax / top-k runs inside the launch and the routing is written to
  * idx32 [T, k], top_k_weights [T, k] bf16 and idx64 [T, k] (optional); without, idx64_in
- * gives it and idx32 receives a copy. Replaces _topk (fused.py:554-570) and
- * _moe_up_kernel with FUSE_TOPK (fused.py:582-632). */
+ * gives it and idx32 receives a copy. With sh_gate / sh_up ([IS, H], IS a multiple of 512)
+ * the same launch also writes act_sh [T, IS] (then stage 1 is called without them; the bits
+ * are the same either way). Replaces _topk (fused.py:554-570) and _moe_up_kernel with
+ * FUSE_TOPK (fused.py:582-632). */
 int moe_decode_gate_up(const void* x, int T, int H, int E, int k, int I, const void* logits,
                        int n_pack, const long long* idx64_in, const void* gate_up,
                        const float* gu_scale, int wdtype, int* idx32, void* top_k_weights,
-                       long long* idx64, void* act, void* stream);
+                       long long* idx64, void* act, const void* sh_gate, const void* sh_up,
+                       int IS, void* act_sh, void* stream);
 
 /* Stage 3: out [T, H] = bf16(bf16(sum_j term_j) + bf16(bf16(sigmoid(seg)) * y_sh))
  * (+ residual), term_j = bf16(w_j * bf16(act_p . Wd[e_p])) under MOE_ROUND_PRODUCT, with

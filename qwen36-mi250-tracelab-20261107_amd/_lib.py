@@ -46,7 +46,8 @@ SIGNATURES: dict[str, tuple] = {
     "moe_decode_fits": (_I, [_I, _I, _I, _I, _I, _I]),
     "moe_decode_router": (_I, [_P, _I, _I, _P, _I, _P, _P, _I, _P, _P, _P]),
     "moe_decode_gate_up": (
-        _I, [_P, _I, _I, _I, _I, _I, _P, _I, _P, _P, _P, _I, _P, _P, _P, _P, _P]),
+        _I, [_P, _I, _I, _I, _I, _I, _P, _I, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _I, _P,
+             _P]),
     "moe_decode_down": (
         _I, [_P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _I, _P, _I, _P, _P, _I, _P, _I, _P, _P]),
     "moe_experts_workspace_bytes": (_SZ, [_I, _I, _I, _I, _I]),

@@ -18,6 +18,7 @@ struct DecodeArgs {
   const float* dn_scale;   // [E, H]
   int fp8;
   const uint16_t *sh_gate, *sh_up, *sh_down;  // shared expert (null: routed experts only)
+  int sh_in_gate_up;  // shared gate/up rows in the K2 launch instead of the K1 launch
   const uint16_t* residual;                   // [T, H] or null
   int round_w;
   uint16_t* logits;          // [T, n_pack]: written by K1, read by K2 / K3 (null: ids_in)

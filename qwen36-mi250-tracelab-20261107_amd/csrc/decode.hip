@@ -138,7 +138,9 @@ __global__ __launch_bounds__(64) void k_dec_router(DecodeArgs a) {
 
 // ------------------------------------------------------------------------------- K2
 
-// grid: P slots x (I / 4) row blocks; slots past the number of distinct experts exit.
+// grid: [IS / 4 shared row blocks when sh_in_gate_up] + P slots x (I / 4) row blocks; slots
+// past the number of distinct experts exit. The shared expert's workgroups need no routing:
+// their weight rows stream while the routed workgroups are still routing.
 template <int NT, int HC, bool FP8, int EPL>
 __global__ __launch_bounds__(kDecThreads) void k_dec_gate_up(DecodeArgs a) {
   __shared__ int s_idx[64];
@@ -147,8 +149,7 @@ __global__ __launch_bounds__(kDecThreads) void k_dec_gate_up(DecodeArgs a) {
   const int H = HC * 512;
   const int P = a.T * a.k;
   const int nrb = a.I / 4;
-  const int slot = blockIdx.x / nrb;
-  const int n = (blockIdx.x - slot * nrb) * 4 + wave;
+  const int nsh = a.sh_in_gate_up && a.sh_gate ? a.IS / 4 : 0;
 
   // token rows: independent of the routing, requested first
   uint4 xv[NT][HC];
@@ -157,6 +158,34 @@ __global__ __launch_bounds__(kDecThreads) void k_dec_gate_up(DecodeArgs a) {
 #pragma unroll
     for (int c = 0; c < HC; ++c)
       xv[t][c] = ld16(a.x + (long long)min(t, a.T - 1) * H + c * 512 + lane * 8);
+
+  if ((int)blockIdx.x < nsh) {
+    // shared gate/up row pair n: the same dot products, in the same order, as in k_dec_router
+    const int n = blockIdx.x * 4 + wave;
+    const uint16_t* rg = a.sh_gate + (long long)n * H;
+    const uint16_t* ru = a.sh_up + (long long)n * H;
+    uint4 wg[HC], wu[HC];
+#pragma unroll
+    for (int c = 0; c < HC; ++c) wg[c] = ld16_stream(rg + c * 512 + lane * 8);
+#pragma unroll
+    for (int c = 0; c < HC; ++c) wu[c] = ld16_stream(ru + c * 512 + lane * 8);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      float sg = 0.f, su = 0.f;
+#pragma unroll
+      for (int c = 0; c < HC; ++c) {
+        sg = dot8(wg[c], xv[t][c], sg);
+        su = dot8(wu[c], xv[t][c], su);
+      }
+      sg = wave_sum(sg);
+      su = wave_sum(su);
+      if (lane == 0 && t < a.T) a.act_sh[(long long)t * a.IS + n] = f2bf_bits(swiglu(sg, su));
+    }
+    return;
+  }
+  const int bid = blockIdx.x - nsh;
+  const int slot = bid / nrb;
+  const int n = (bid - slot * nrb) * 4 + wave;
 
   // key: the expert of pair `lane` (lanes < P); distinct: the pairs' experts are known to
   // differ (one token routed here)
@@ -169,7 +198,7 @@ __global__ __launch_bounds__(kDecThreads) void k_dec_gate_up(DecodeArgs a) {
     route_row<EPL>(a.logits, a.E, a.k, lane, my_idx, my_w);
     key = my_idx;
     distinct = true;
-    if (blockIdx.x == 0 && wave == 0 && lane < a.k) {
+    if (bid == 0 && wave == 0 && lane < a.k) {
       a.idx32[lane] = my_idx;
       a.wts[lane] = f2bf_bits(my_w);
       if (a.idx64) a.idx64[lane] = my_idx;
@@ -183,7 +212,7 @@ __global__ __launch_bounds__(kDecThreads) void k_dec_gate_up(DecodeArgs a) {
         if (lane < a.k) {
           const int p = wave * a.k + lane;
           s_idx[p] = my_idx;
-          if (blockIdx.x == 0) {
+          if (bid == 0) {
             a.idx32[p] = my_idx;
             a.wts[p] = f2bf_bits(my_w);
             if (a.idx64) a.idx64[p] = my_idx;
@@ -194,7 +223,7 @@ __global__ __launch_bounds__(kDecThreads) void k_dec_gate_up(DecodeArgs a) {
       const long long v = a.ids_in[threadIdx.x];
       const int e = (int)(v < 0 ? 0 : (v >= a.E ? a.E - 1 : v));
       s_idx[threadIdx.x] = e;
-      if (blockIdx.x == 0) a.idx32[threadIdx.x] = e;
+      if (bid == 0) a.idx32[threadIdx.x] = e;
     }
     __syncthreads();
     key = lane < P ? s_idx[lane] : -1;
@@ -458,7 +487,7 @@ bool down_legacy() {
 
 template <int NT>
 hipError_t launch_router_nt(const DecodeArgs& a, hipStream_t s) {
-  const int grid = a.n_pack + (a.sh_gate ? a.IS : 0);
+  const int grid = a.n_pack + (a.sh_gate && !a.sh_in_gate_up ? a.IS : 0);
   switch (a.H / 512) {
 #define L(HC)                                                                             \
   case HC:                                                                                \
@@ -474,7 +503,7 @@ hipError_t launch_router_nt(const DecodeArgs& a, hipStream_t s) {
 
 template <int NT, bool FP8>
 hipError_t launch_gate_up_nt(const DecodeArgs& a, hipStream_t s) {
-  const int grid = a.T * a.k * (a.I / 4);
+  const int grid = a.T * a.k * (a.I / 4) + (a.sh_gate && a.sh_in_gate_up ? a.IS / 4 : 0);
   const int epl = a.logits ? (a.E + 63) / 64 : 1;
 #define LG(HC, EPL)                                                                         \
   if (a.H / 512 == HC && epl <= EPL) {                                                      \

@@ -100,6 +100,14 @@ bool block_side_enabled(int T, bool fp8, int bm) {
   return fp8 || bm == prefill_tile_rows();
 }
 
+// Decode block: the shared expert's gate/up rows go to the gate_up launch, where they stream
+// while the routed workgroups route (MOE_DECODE_SHARED=router keeps them in the router
+// launch).
+bool decode_shared_in_gate_up() {
+  const char* env = getenv("MOE_DECODE_SHARED");
+  return !(env && env[0] == 'r');
+}
+
 size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
 
 // The first kSyncBytes of every workspace are reserved for cross-workgroup counters: zero
@@ -549,8 +557,11 @@ int moe_decode_router(const void* x, int T, int H, const void* w_pack, int n_pac
 int moe_decode_gate_up(const void* x, int T, int H, int E, int k, int I, const void* logits,
                        int n_pack, const long long* idx64_in, const void* gate_up,
                        const float* gu_scale, int wdtype, int* idx32, void* top_k_weights,
-                       long long* idx64, void* act, void* stream) {
+                       long long* idx64, void* act, const void* sh_gate, const void* sh_up,
+                       int IS, void* act_sh, void* stream) {
   CHECK_ARG(x && gate_up && idx32 && act, "null pointer");
+  CHECK_ARG(!sh_gate || (sh_up && act_sh && IS >= 512 && IS % 512 == 0),
+            "shared gate needs shared up, act_sh and IS a multiple of 512");
   CHECK_ARG(logits || idx64_in, "need logits or a given routing");
   CHECK_ARG(!logits || (top_k_weights && n_pack >= E), "routing outputs / n_pack");
   CHECK_ARG(wdtype == MOE_WEIGHTS_BF16 || (wdtype == MOE_WEIGHTS_FP8_E4M3 && gu_scale),
@@ -567,6 +578,11 @@ int moe_decode_gate_up(const void* x, int T, int H, int E, int k, int I, const v
   d.wts = static_cast<uint16_t*>(top_k_weights);
   d.idx64 = idx64;
   d.act = static_cast<uint16_t*>(act);
+  d.IS = IS;
+  d.sh_gate = static_cast<const uint16_t*>(sh_gate);
+  d.sh_up = static_cast<const uint16_t*>(sh_up);
+  d.act_sh = static_cast<uint16_t*>(act_sh);
+  d.sh_in_gate_up = sh_gate != nullptr;
   CHECK_ARG(decode_fits(d), "decode gate_up shape (T=%d H=%d E=%d k=%d I=%d) not supported", T,
             H, E, k, I);
   return hip_check(launch_decode_gate_up(d, (hipStream_t)stream), "decode gate_up launch");
@@ -773,6 +789,7 @@ int moe_block_forward(const void* x, int T, int H, int E, int k, int I, int IS,
     d.sh_gate = static_cast<const uint16_t*>(sh_gate);
     d.sh_up = static_cast<const uint16_t*>(sh_up);
     d.sh_down = static_cast<const uint16_t*>(sh_down);
+    d.sh_in_gate_up = decode_shared_in_gate_up();
     d.residual = static_cast<const uint16_t*>(residual);
     d.round_w = mode == MOE_ROUND_PRODUCT;
     d.logits = lg;

@@ -315,10 +315,12 @@ def decode_router(x: torch.Tensor, w_pack: torch.Tensor, shared: tuple | None = 
 
 
 def decode_gate_up(x: torch.Tensor, gate_up: torch.Tensor, top_k: int, *, logits=None,
-                   experts: int | None = None, top_k_index=None, scale=None):
+                   experts: int | None = None, top_k_index=None, scale=None, shared=None):
     """(act [T*k, I], idx32 [T, k], top_k_weights [T, k] bf16 or None, top_k_index int64
     or None). With ``logits`` the routing (softmax / top-k over the first ``experts``
-    columns) runs inside the launch; else ``top_k_index`` gives it."""
+    columns) runs inside the launch; else ``top_k_index`` gives it. With
+    ``shared=(gate_proj.weight, up_proj.weight)`` the launch also computes the shared
+    expert's activation, returned as a fifth item act_shared [T, IS]."""
     _need_cuda(x, gate_up)
     x = _bf16(x, "x")
     gu, gus, wd = expert_weight(gate_up, scale, "gate_up")
@@ -339,10 +341,19 @@ def decode_gate_up(x: torch.Tensor, gate_up: torch.Tensor, top_k: int, *, logits
         if top_k_index is None:
             raise ValueError("decode_gate_up needs logits or top_k_index")
         idx_in = top_k_index.to(torch.long).contiguous()
+    sg = su = act_sh = None
+    inter_s = 0
+    if shared is not None:
+        sg, su = (_bf16(t, "shared weight") for t in shared)
+        inter_s = sg.shape[0]
+        act_sh = torch.empty((tokens, inter_s), dtype=torch.bfloat16, device=dev)
     check(_lib.load().moe_decode_gate_up(ptr(x), tokens, hidden, experts, top_k, two_i // 2,
                                          ptr(logits), n_pack, ptr(idx_in), ptr(gu), ptr(gus), wd,
-                                         ptr(idx32), ptr(wts), ptr(idx64), ptr(act),
-                                         stream_of(x)), "decode_gate_up")
+                                         ptr(idx32), ptr(wts), ptr(idx64), ptr(act), ptr(sg),
+                                         ptr(su), inter_s, ptr(act_sh), stream_of(x)),
+          "decode_gate_up")
+    if shared is not None:
+        return act, idx32, wts, idx64, act_sh
     return act, idx32, wts, idx64
 
 

@@ -157,16 +157,23 @@ def test_decode_fp8_block(pkg, dev, layer, T):
         assert max_abs(out, t_out) <= 4e-3
 
 
-def test_decode_stages_compose_to_block(pkg, dev, layer):
+@pytest.mark.parametrize("shared_in", ["router", "gate_up"])
+def test_decode_stages_compose_to_block(pkg, dev, layer, shared_in):
     """The operator-level stages (decode_router -> decode_gate_up -> decode_down) give the
-    block's bits."""
+    block's bits, with the shared gate/up rows in either of the first two launches."""
     mlp = _mlp(layer, dev)
     x = torch.randn(2, 2048, generator=torch.Generator().manual_seed(3)).to(BF16).to(dev)
     pack = pkg.block.pack_router(mlp)
     sh = mlp.shared_expert
-    logits, act_sh = pkg.ops.decode_router(x, pack, shared=(sh.gate_proj.weight, sh.up_proj.weight))
-    act, idx32, wts, idx64 = pkg.ops.decode_gate_up(x, layer["gate_up"], 8, logits=logits,
-                                                    experts=256)
+    sh_gu = (sh.gate_proj.weight, sh.up_proj.weight)
+    if shared_in == "router":
+        logits, act_sh = pkg.ops.decode_router(x, pack, shared=sh_gu)
+        act, idx32, wts, idx64 = pkg.ops.decode_gate_up(x, layer["gate_up"], 8, logits=logits,
+                                                        experts=256)
+    else:
+        logits, _ = pkg.ops.decode_router(x, pack)
+        act, idx32, wts, idx64, act_sh = pkg.ops.decode_gate_up(
+            x, layer["gate_up"], 8, logits=logits, experts=256, shared=sh_gu)
     out = pkg.ops.decode_down(act, 2, 8, layer["down"], idx32, wts,
                               shared=(sh.down_proj.weight, act_sh), logits=logits, experts=256)
     b_out, b_idx, b_wts, b_lg = pkg.block.moe(x, mlp, 8, decode=True, return_routing=True)
