@@ -40,8 +40,6 @@ struct GemmArgs {
   int topk, P, E, T;
   int nrb;           // weight-row blocks per tile (set by the launcher)
   int MTgrid;        // tiles the grid covers (set by the launcher)
-  int dbg;           // 0; tuning experiments only (MOE_GEMM_DEBUG): 1 skip token-row
-                     // loads, 4 skip per-chunk barriers
 };
 
 // Launches k_expert_gemm over max_tiles tiles of at most bm (16, 32, 64 or 128) sorted rows.

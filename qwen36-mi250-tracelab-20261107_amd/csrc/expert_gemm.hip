@@ -230,12 +230,12 @@ void k_expert_gemm(GemmArgs args) {
           for (int s = 0; s < LPC8; ++s) aring[cc][s] = ld16(wp8 + (c + R) * KC + s * 64);
         }
       }
-      if (c + 1 + R < nch && !(args.dbg & 1)) {
+      if (c + 1 + R < nch) {
 #pragma unroll
         for (int i = 0; i < STG; ++i)
           if (sneed[i]) bring[(cc + 1) % R][i] = ld16(xin + srow[i] + (c + 1 + R) * KC);
       }
-      if (!(args.dbg & 4)) __syncthreads();
+      __syncthreads();
     }
   }
 
@@ -388,8 +388,6 @@ bool env_cfg(int role, Cfg* out) {
 hipError_t launch_expert_gemm(int mode, int role, int bm, const GemmArgs& a_in, int max_tiles,
                               hipStream_t st) {
   GemmArgs a = a_in;
-  if (const char* dbg = getenv("MOE_GEMM_DEBUG"))
-    if (role != kRoleRouter) a.dbg = atoi(dbg);
   const bool fp8 = (a.op[0].N > 0 && a.op[0].fp8) || (a.op[1].N > 0 && a.op[1].fp8);
   if (a.op[0].N > 0 && a.op[1].N > 0 && a.op[0].fp8 != a.op[1].fp8)
     return hipErrorInvalidValue;  // one weight type per launch (the caller splits)

@@ -29,10 +29,6 @@
 #include "moe_common.h"
 #include "expert_gemm.h"
 
-#ifndef MOE_PF_TRACE
-#define MOE_PF_TRACE(tag, c)  // timing hook of the kernel's own benchmarks; no-op here
-#endif
-
 namespace moe {
 
 namespace {
@@ -256,15 +252,12 @@ __global__ __launch_bounds__(kThreads, 1) void k_prefill_gemm(GemmArgs args) {
   frags_ready(f0);
   auto step = [&](int j, Frags& cur, Frags& nxt) {
     const bool more = j + 1 < nk;
-    MOE_PF_TRACE(0, j);
     if (more) {
       const int jn = j + 1, dn = jn >> 1;
       if ((jn & 1) == 0) {
         // chunk dn: younger than B(dn) is A(dn + 1) if it was issued
         wait_loads(4 * (dn + 1 < nd));
-        MOE_PF_TRACE(1, j);
         __builtin_amdgcn_s_barrier();
-        MOE_PF_TRACE(2, j);
         if (dn + kAheadB < nd) issue_b(dn + kAheadB);
         if (dn + kAheadA < nd) issue_a(dn + kAheadA);
       }
@@ -273,9 +266,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_prefill_gemm(GemmArgs args) {
                  lds_base + (kStagesA + dn % kStagesB) * kOpStage + ro, wm, wn, nxt);
     }
     mma_frags(cur, nb, acc);
-    MOE_PF_TRACE(3, j);
     if (more) frags_ready(nxt);
-    MOE_PF_TRACE(4, j);
   };
   for (int j = 0; j < nk; j += 2) {
     step(j, f0, f1);
@@ -337,7 +328,6 @@ bool prefill_fits(int mode, const GemmOperand& op) {
 hipError_t launch_prefill_gemm(int mode, const GemmArgs& a_in, int max_tiles, hipStream_t st) {
   GemmArgs a = a_in;
   if (!prefill_fits(mode, a.op[0]) || !prefill_fits(mode, a.op[1])) return hipErrorInvalidValue;
-  if (const char* env = getenv("MOE_PREFILL_DEBUG")) a.dbg = atoi(env);  // timing experiments
   const int out_per_wg = mode == kModeSwiglu ? PBN / 2 : PBN;
   const int nmax = a.op[0].N > a.op[1].N ? a.op[0].N : a.op[1].N;
   a.nrb = (nmax + out_per_wg - 1) / out_per_wg;
