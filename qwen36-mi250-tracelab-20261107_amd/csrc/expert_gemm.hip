@@ -402,7 +402,6 @@ hipError_t launch_expert_gemm(int mode, int role, int bm, const GemmArgs& a_in, 
     forced.tokb = tokb;
     prefs[n++] = forced;
   }
-  (void)0;
   // fp8 weights move half the bytes per K element: 128-element chunks keep as many bytes
   // in flight as the bf16 64-element ones.
   const int rr = fp8 ? 8 : 4;  // fp8: 64-element chunks are half the bytes, twice as many
@@ -413,10 +412,16 @@ hipError_t launch_expert_gemm(int mode, int role, int bm, const GemmArgs& a_in, 
     prefs[n++] = {1, 1, 1, 128};
   } else if (tokb == 2) {
     if (fp8) {
-      // fp8 32-token tiles: four row groups per workgroup, 256-element chunks, two-deep
-      // ring (fastest of the fp8 configurations measured at the 40-layer T=32 shape)
-      prefs[n++] = {4, 1, 2, 256, 2};
-      prefs[n++] = {4, 1, 2, 128, 4};
+      // fp8 32-token tiles: four row groups per workgroup; gate_up with 128-element chunks
+      // four deep, down (K = 512) with 256-element chunks two deep (the fastest measured at
+      // the 40-layer T=32 shape: 157 against 161 µs per layer with 256 x 2 for gate_up)
+      if (role == kRoleDown) {
+        prefs[n++] = {4, 1, 2, 256, 2};
+        prefs[n++] = {4, 1, 2, 128, 4};
+      } else {
+        prefs[n++] = {4, 1, 2, 128, 4};
+        prefs[n++] = {4, 1, 2, 256, 2};
+      }
     } else {
       prefs[n++] = role == kRoleDown ? Cfg{2, 1, 2, 64, rr} : Cfg{2, 2, 2, 64, rr};
     }
