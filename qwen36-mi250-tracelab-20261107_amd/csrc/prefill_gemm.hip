@@ -14,17 +14,20 @@
 // puts gate rows in blocks 0-1 and the matching up rows in blocks 2-3 of a wave, so the
 // epilogue pairs them in registers.
 //
-// Pipeline. K runs in chunks of 32 (one MFMA k-step). A chunk of both operands (256 + 256
-// rows x 64 B) is 32 blocks of 16 rows x 64 B; each block is one 1 KiB global -> LDS DMA
-// load of a wave (global_load_lds_dwordx4: no registers on the way), and an MFMA fragment
-// is one 1 KiB LDS read of a block. Inside a block the four 16-byte units of row r sit in
-// the order u ^ ((r >> 2) & 3), which makes the fragment reads bank-conflict free. Four LDS
-// stages: while chunk c is multiplied, the fragments of chunk c + 1 are being read into
-// registers and the DMA loads of chunks c + 2 and c + 3 are in flight.
-// The fragment reads are issued by inline asm with explicit lgkmcnt waits and the stages are
-// fenced by explicit vmcnt waits, because the compiler's own waits would drain every
-// outstanding DMA load before each LDS read.
+// Pipeline. K runs in DMA chunks of 64 (128 bytes of each row). A chunk of one operand is
+// 32 groups of 8 rows x 128 B; each group is one 1 KiB global -> LDS DMA load of a wave
+// (global_load_lds_dwordx4: no registers on the way), lane l writing physical 16-byte unit
+// l & 7 of row l >> 3, which holds logical unit (l & 7) ^ row, so the MFMA fragment reads
+// (16 rows x one logical unit = one 1 KiB LDS read per 16 x 32 fragment) are bank-conflict
+// free. Weight ring of 3 stages (chunk c + 2 requested while c is multiplied), token-row
+// ring of 2 (c + 1): 160 KiB. The fragments of the next k-step (32) are read while the
+// current one is multiplied. The fragment reads are issued by inline asm with explicit
+// lgkmcnt waits and the stages are fenced by explicit vmcnt waits, because the compiler's
+// own waits would drain every outstanding DMA load before each LDS read.
+#include <stdint.h>
 #include <stdlib.h>
+
+#include <mutex>
 
 #include "moe_common.h"
 #include "expert_gemm.h"
@@ -325,6 +328,23 @@ bool prefill_fits(int mode, const GemmOperand& op) {
   return !op.fp8 && rows_ok && op.K % PKC == 0;
 }
 
+namespace {
+// The kernels' dynamic LDS above the default limit, allowed once per device and mode.
+hipError_t allow_lds(const void* fn, int mode, int bytes) {
+  static std::mutex mu;
+  static uint64_t done[2] = {0, 0};  // bit d: device d
+  int dev = 0;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return err;
+  if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(mu);
+  if (done[mode] >> dev & 1) return hipSuccess;
+  err = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (err == hipSuccess) done[mode] |= uint64_t(1) << dev;
+  return err;
+}
+}  // namespace
+
 hipError_t launch_prefill_gemm(int mode, const GemmArgs& a_in, int max_tiles, hipStream_t st) {
   GemmArgs a = a_in;
   if (!prefill_fits(mode, a.op[0]) || !prefill_fits(mode, a.op[1])) return hipErrorInvalidValue;
@@ -335,23 +355,15 @@ hipError_t launch_prefill_gemm(int mode, const GemmArgs& a_in, int max_tiles, hi
   const size_t lds = (size_t)kLdsBytes;
   a.MTgrid = max_tiles;
   const long long grid = (long long)((max_tiles + kXcds - 1) / kXcds) * kXcds * a.nrb;
-  if (mode == kModeSwiglu) {
-    static bool attr = false;
-    if (!attr) {
-      hipFuncSetAttribute(reinterpret_cast<const void*>(&k_prefill_gemm<kModeSwiglu>),
-                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-      attr = true;
-    }
+  const void* fn = mode == kModeSwiglu
+                       ? reinterpret_cast<const void*>(&k_prefill_gemm<kModeSwiglu>)
+                       : reinterpret_cast<const void*>(&k_prefill_gemm<kModePlain>);
+  hipError_t err = allow_lds(fn, mode, (int)lds);
+  if (err != hipSuccess) return err;
+  if (mode == kModeSwiglu)
     hipLaunchKernelGGL(k_prefill_gemm<kModeSwiglu>, dim3((unsigned)grid), dim3(kThreads), lds, st, a);
-  } else {
-    static bool attr = false;
-    if (!attr) {
-      hipFuncSetAttribute(reinterpret_cast<const void*>(&k_prefill_gemm<kModePlain>),
-                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-      attr = true;
-    }
+  else
     hipLaunchKernelGGL(k_prefill_gemm<kModePlain>, dim3((unsigned)grid), dim3(kThreads), lds, st, a);
-  }
   return hipGetLastError();
 }
 
