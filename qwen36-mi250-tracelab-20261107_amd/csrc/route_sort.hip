@@ -83,6 +83,30 @@ __global__ __launch_bounds__(kSortThreads) void k_sort_scan(int* __restrict__ bc
   // whose loads are all in flight together (one memory round trip per group, not per block).
   constexpr int G = 16;
   int e = threadIdx.x;
+  if (nblocks <= 2 * G) {
+    // up to 32 blocks: one round trip, the counts kept in registers for the final bases
+    int c[2 * G], base[2 * G];
+    int acc = 0;
+    if (e < E) {
+#pragma unroll
+      for (int i = 0; i < 2 * G; ++i) c[i] = i < nblocks ? bcnt[(long long)i * E + e] : 0;
+#pragma unroll
+      for (int i = 0; i < 2 * G; ++i) {
+        base[i] = acc;
+        acc += c[i];
+      }
+      hist[e] = acc;
+    }
+    __syncthreads();
+    build_table(hist, E, P, T, bm, has_shared, offs, counts_g, offsets_g, table, MT, tmp);
+    if (e < E) {
+      const int o = offs[e];
+#pragma unroll
+      for (int i = 0; i < 2 * G; ++i)
+        if (i < nblocks) bcnt[(long long)i * E + e] = base[i] + o;
+    }
+    return;
+  }
   if (e < E) {
     int acc = 0;
     for (int b0 = 0; b0 < nblocks; b0 += G) {
