@@ -34,7 +34,9 @@ namespace moe {
 
 namespace {
 
-constexpr int kDecThreads = 256;  // K2 / K3: four waves, one row (pair) each
+constexpr int kDecThreads = 256;  // K3 (several tokens): four waves, one row each
+constexpr int kGuWaves = 4;       // K2: waves per workgroup, one gate/up row pair each
+static_assert(kGuWaves >= kDecMaxTokens, "K2 routes one token per wave");
 
 __device__ __forceinline__ float dot8(uint4 w, uint4 x, float acc) {
   acc = fmaf(bf_lo(w.x), bf_lo(x.x), acc);
@@ -138,18 +140,18 @@ __global__ __launch_bounds__(64) void k_dec_router(DecodeArgs a) {
 
 // ------------------------------------------------------------------------------- K2
 
-// grid: [IS / 4 shared row blocks when sh_in_gate_up] + P slots x (I / 4) row blocks; slots
-// past the number of distinct experts exit. The shared expert's workgroups need no routing:
-// their weight rows stream while the routed workgroups are still routing.
+// grid: [IS / kGuWaves shared row blocks when sh_in_gate_up] + P slots x (I / kGuWaves) row
+// blocks; slots past the number of distinct experts exit. The shared expert's workgroups
+// need no routing: their weight rows stream while the routed workgroups are still routing.
 template <int NT, int HC, bool FP8, int EPL>
-__global__ __launch_bounds__(kDecThreads) void k_dec_gate_up(DecodeArgs a) {
+__global__ __launch_bounds__(64 * kGuWaves) void k_dec_gate_up(DecodeArgs a) {
   __shared__ int s_idx[64];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int H = HC * 512;
   const int P = a.T * a.k;
-  const int nrb = a.I / 4;
-  const int nsh = a.sh_in_gate_up && a.sh_gate ? a.IS / 4 : 0;
+  const int nrb = a.I / kGuWaves;
+  const int nsh = a.sh_in_gate_up && a.sh_gate ? a.IS / kGuWaves : 0;
 
   // token rows: independent of the routing, requested first
   uint4 xv[NT][HC];
@@ -161,7 +163,7 @@ __global__ __launch_bounds__(kDecThreads) void k_dec_gate_up(DecodeArgs a) {
 
   if ((int)blockIdx.x < nsh) {
     // shared gate/up row pair n: the same dot products, in the same order, as in k_dec_router
-    const int n = blockIdx.x * 4 + wave;
+    const int n = blockIdx.x * kGuWaves + wave;
     const uint16_t* rg = a.sh_gate + (long long)n * H;
     const uint16_t* ru = a.sh_up + (long long)n * H;
     uint4 wg[HC], wu[HC];
@@ -185,7 +187,7 @@ __global__ __launch_bounds__(kDecThreads) void k_dec_gate_up(DecodeArgs a) {
   }
   const int bid = blockIdx.x - nsh;
   const int slot = bid / nrb;
-  const int n = (bid - slot * nrb) * 4 + wave;
+  const int n = (bid - slot * nrb) * kGuWaves + wave;
 
   // key: the expert of pair `lane` (lanes < P); distinct: the pairs' experts are known to
   // differ (one token routed here)
@@ -503,11 +505,12 @@ hipError_t launch_router_nt(const DecodeArgs& a, hipStream_t s) {
 
 template <int NT, bool FP8>
 hipError_t launch_gate_up_nt(const DecodeArgs& a, hipStream_t s) {
-  const int grid = a.T * a.k * (a.I / 4) + (a.sh_gate && a.sh_in_gate_up ? a.IS / 4 : 0);
+  const int grid =
+      a.T * a.k * (a.I / kGuWaves) + (a.sh_gate && a.sh_in_gate_up ? a.IS / kGuWaves : 0);
   const int epl = a.logits ? (a.E + 63) / 64 : 1;
 #define LG(HC, EPL)                                                                         \
   if (a.H / 512 == HC && epl <= EPL) {                                                      \
-    hipLaunchKernelGGL((k_dec_gate_up<NT, HC, FP8, EPL>), dim3(grid), dim3(kDecThreads), 0, s, a); \
+    hipLaunchKernelGGL((k_dec_gate_up<NT, HC, FP8, EPL>), dim3(grid), dim3(64 * kGuWaves), 0, s, a); \
     return hipGetLastError();                                                               \
   }
 #define LH(HC) LG(HC, 1) LG(HC, 2) LG(HC, 4) LG(HC, 8)
