@@ -380,3 +380,40 @@ def test_calls_leave_sync_area_zero_and_repeat(pkg, dev, full_layer):
         assert torch.equal(a, b), T
     for ws in pkg._lib._WORKSPACES.values():
         assert int(ws[: pkg._lib.SYNC_BYTES].count_nonzero()) == 0
+
+
+def test_zero_tokens(pkg, dev):
+    """Empty batches: every surface returns an empty [0, H] output without launching."""
+    H, E, K, I = 256, 16, 4, 128
+    w = orc.make_weights(H, E, I, I, seed=3)
+    mlp = _gpu_mlp(w, dev)
+    x = torch.empty((0, H), dtype=BF16, device=dev)
+    out = pkg.block.moe(x, mlp, K)
+    assert out.shape == (0, H)
+    idx = torch.empty((0, K), dtype=torch.long, device=dev)
+    wts = torch.empty((0, K), dtype=BF16, device=dev)
+    got = pkg.ops.experts(x, idx, wts, w["gate_up"].to(dev), w["down"].to(dev),
+                          round_products=True)
+    torch.cuda.synchronize()
+    assert got.shape == (0, H)
+
+
+@pytest.mark.parametrize("E,K,T", [(8, 8, 3), (8, 8, 40), (48, 1, 5), (48, 1, 70), (64, 2, 1)])
+def test_block_edge_routings(pkg, dev, E, K, T):
+    """Every expert chosen by every token (k = E), one expert per token (k = 1), and an
+    expert count that is not a multiple of the 64-lane wave: routing bit-exact given the
+    logits, values against the fp32 oracle."""
+    _say("block edge", E, K, T)
+    H, I = 256, 128
+    w = orc.make_weights(H, E, I, I, seed=E + K)
+    g = torch.Generator().manual_seed(T + 11)
+    x = torch.randn(T, H, generator=g).to(BF16)
+    out, idx, wts, logits = pkg.block.moe(x.to(dev), _gpu_mlp(w, dev), K, return_routing=True)
+    torch.cuda.synchronize()
+    lg = logits.cpu()[:, :E]
+    ref_w, ref_i = orc.route(lg, K)
+    assert torch.equal(idx.cpu(), ref_i)
+    assert torch.equal(wts.cpu(), ref_w)
+    f32 = orc.block_fp32(x, w, ref_i, logits=lg)
+    _say(f" vs fp32 max {max_abs(out, f32):.3g} mean-rel {mean_rel(out, f32):.3g}")
+    assert max_abs(out, f32) <= 2e-2 and mean_rel(out, f32) <= 5e-3
