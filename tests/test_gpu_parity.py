@@ -32,7 +32,7 @@ def _say(*a):
 # ----------------------------------------------------------------------------- routing
 
 
-@pytest.mark.parametrize("E,k", [(256, 8), (16, 4), (8, 2), (64, 8), (128, 1)])
+@pytest.mark.parametrize("E,k", [(256, 8), (16, 4), (8, 2), (64, 8), (128, 1), (512, 8)])
 @pytest.mark.parametrize("seed", [0, 1])
 def test_route_bitexact(pkg, dev, E, k, seed):
     _say("route", E, k, seed)
@@ -98,7 +98,7 @@ def test_route_bruteforce_small(pkg, dev):
 
 
 SORT_CASES = [(1, 256, 8), (4, 16, 4), (64, 256, 8), (75, 16, 4), (300, 16, 4), (513, 256, 8),
-              (1000, 256, 8), (2049, 64, 2)]
+              (1000, 256, 8), (2049, 64, 2), (700, 512, 8), (4096, 256, 8)]
 
 
 @pytest.mark.parametrize("T,E,k", SORT_CASES)
