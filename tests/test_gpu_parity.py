@@ -417,3 +417,47 @@ def test_block_edge_routings(pkg, dev, E, K, T):
     f32 = orc.block_fp32(x, w, ref_i, logits=lg)
     _say(f" vs fp32 max {max_abs(out, f32):.3g} mean-rel {mean_rel(out, f32):.3g}")
     assert max_abs(out, f32) <= 2e-2 and mean_rel(out, f32) <= 5e-3
+
+
+def _sweep_cases():
+    """A fixed, seeded spread of block shapes over every regime (decode path, 16/32-row
+    expert GEMM tiles, prefill tiles): hidden, experts, top-k, intermediate, shared
+    intermediate, tokens."""
+    import random
+
+    rnd = random.Random(2026)
+    cases = []
+    for _ in range(20):
+        H = rnd.choice([256, 512, 1024])
+        E = rnd.choice([8, 16, 40, 64, 96])
+        k = rnd.choice([1, 2, 4, 8] if E >= 8 else [1, 2])
+        I = rnd.choice([128, 256, 512])
+        IS = rnd.choice([128, 512])
+        T = rnd.choice([1, 2, 4, 7, 33, 130, 600])
+        cases.append((H, E, k, I, IS, T))
+    return cases
+
+
+@pytest.mark.parametrize("H,E,K,I,IS,T", _sweep_cases())
+def test_block_shape_sweep(pkg, dev, H, E, K, I, IS, T):
+    """Routing bit-exact given the logits and values against the fp32 oracle over a seeded
+    spread of shapes."""
+    _say("sweep", H, E, K, I, IS, T)
+    w = orc.make_weights(H, E, I, IS, seed=H + E + K + I + IS + T)
+    g = torch.Generator().manual_seed(T * 31 + E)
+    x = torch.randn(T, H, generator=g).to(BF16)
+    out, idx, wts, logits = pkg.block.moe(x.to(dev), _gpu_mlp(w, dev), K, return_routing=True)
+    torch.cuda.synchronize()
+    lg = logits.cpu()[:, :E]
+    ref_w, ref_i = orc.route(lg, K)
+    assert torch.equal(idx.cpu(), ref_i)
+    assert torch.equal(wts.cpu(), ref_w)
+    f32 = orc.block_fp32(x, w, ref_i, logits=lg)
+    # the reference torch path (bf16 rounding points) on the same routing: its own mean-rel
+    # to fp32 sets the bar where the outputs are small (mean-rel 5e-3 or 1.1x that)
+    wc, ic = orc.compact_experts(w, ref_i)
+    ref = orc.block_bf16_routed(x, wc, ic, wts.cpu(), logits.cpu()[:, E:E + 1])
+    ours, theirs = mean_rel(out, f32), mean_rel(ref, f32)
+    _say(f" vs fp32 max {max_abs(out, f32):.3g} mean-rel {ours:.3g} (reference path {theirs:.3g})")
+    assert max_abs(out, f32) <= 2e-2
+    assert ours <= max(5e-3, 1.1 * theirs)
