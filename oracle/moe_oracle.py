@@ -15,8 +15,16 @@ the reference path the MI355X kernels replace, with each function citing what it
 Two modes of the block: ``block_bf16`` rounds where the torch bf16 reference rounds
 (F.linear / bmm outputs, activation, products) and is the parity target for values;
 ``block_fp32`` computes the experts in fp32 from the same routing and is the tolerance
-reference the north star names. How each function is pinned is stated in DESIGN.md and
-tested in tests/test_oracle.py.
+reference the north star names.
+
+How each function is pinned (tests/test_oracle.py): ``route`` by brute force on tie-heavy
+rows, explicit tie cases, torch.topk up to ties and float64 renormalisation; ``sort_pairs``
+by the closed-form tile table and stable-permutation invariants; ``batched_mm_experts`` bit
+for bit against Transformers' batched_mm_experts_forward; ``sorted_experts`` /
+``padded_experts`` against each other and Transformers' eager experts loop; ``block_bf16``
+bit for bit against Transformers' Qwen3_5MoeSparseMoeBlock; ``block_fp32`` against a
+float64 restatement; the e4m3 codec against all 256 encodings of torch's cast. Nothing here
+is left parity unpinned.
 """
 
 from __future__ import annotations
