@@ -190,6 +190,27 @@ def run_config(torch, dev, name, T, layers, steps, warmup, zipf=False, fp8=False
         res["mfma_frac_bf16"] = round(flops / (us_layer * 1e-6) / 1e12 / BF16_PEAK_TFLOPS, 4)
     del graph
 
+    if T <= 4:
+        # the decoder layer's post-attention add + RMSNorm in front of the block: fused into
+        # the router launch against its own launch followed by the block (not the headline)
+        hs = [x.flip(0).roll(1, 1) for x in xs]
+        nw = (torch.randn(H, generator=torch.Generator().manual_seed(3)) * 0.1).to(
+            torch.bfloat16).to(dev)
+
+        def fused_pass():
+            for mlp, x, h in zip(mlps, xs, hs):
+                pkg.block.add_rms_moe(x, h, nw, 1e-6, mlp, K_TOP, decode=True)
+
+        def separate_pass():
+            for mlp, x, h in zip(mlps, xs, hs):
+                total, norm = pkg.ops.add_rms(x, h, nw, 1e-6)
+                pkg.block.moe(norm, mlp, K_TOP, decode=True, residual=total)
+
+        for key, fn in (("add_rms_moe_us", fused_pass), ("add_rms_then_moe_us", separate_pass)):
+            graph = capture(torch, fn)
+            res[key] = round(time_graph(torch, graph, reps, wreps) * 1000.0 / nsteps, 3)
+            del graph
+
     # the dominant kernel alone, as the block launches it: the decode gate_up (routing in the
     # launch, routed experts + the shared expert's gate/up rows) for decode-path shapes, else
     # the grouped gate_up (routed + shared) over the sorted tile table

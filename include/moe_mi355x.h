@@ -180,6 +180,33 @@ int moe_block_forward(const void* x, int T, int H, int E, int k, int I, int IS,
                       void* out, long long* top_k_index, void* top_k_weights, void* logits,
                       void* workspace, size_t workspace_bytes, void* stream);
 
+/* Post-attention residual add + zero-centred RMSNorm: total = bf16(x + h) and
+ * out = bf16(total * rsqrt(mean(total^2) + eps) * (1 + weight)), fp32 in between; h null:
+ * no add (total is not written, the norm is of x). x, h, total, out [T, H] bf16 with
+ * 16-byte-aligned rows, weight [H] bf16, H a multiple of 8 up to 8192; outputs must not
+ * overlap the inputs. Replaces kernels.add_rms (engine/fast/kernels.py:636-650, math of
+ * _add_rms_kernel kernels.py:507-523, as Transformers' Qwen3_5MoeRMSNorm
+ * modeling_qwen3_5_moe.py:801-815). */
+int moe_add_rmsnorm(const void* x, const void* h, const void* weight, int T, int H, float eps,
+                    void* total, void* out, void* stream);
+
+/* The post-attention add_rms and the MoE block of one decoder layer:
+ * (total, norm) = add_rms(x, h, norm_weight, eps), out = total + MoE(norm) (h null: x stands
+ * for total). Replaces `x, h = kernels.add_rms(x, h, post_attention_layernorm.weight, eps)`
+ * followed by the block with x as residual (engine/fast/model.py:888-891; fused.py:1074-1076
+ * with FusedDecode._moe fused.py:887-932). total and norm are written too. On the decode path
+ * the norm runs inside the router launch (no launch of its own); elsewhere one add_rms launch
+ * precedes the block. Other arguments, the workspace (moe_block_workspace_bytes) and the
+ * optional routing outputs are those of moe_block_forward. */
+int moe_block_forward_add_rms(const void* x, const void* h, const void* norm_weight, float eps,
+                              int T, int H, int E, int k, int I, int IS, const void* w_pack,
+                              int n_pack, const void* gate_up, const float* gu_scale,
+                              const void* down, const float* dn_scale, int wdtype,
+                              const void* sh_gate, const void* sh_up, const void* sh_down,
+                              int mode, void* total, void* norm, void* out,
+                              long long* top_k_index, void* top_k_weights, void* logits,
+                              void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -9,6 +9,7 @@ the reference path the MI355X kernels replace, with each function citing what it
 - the engine's experts implementation, /root/reference/engine/experts.py:34-102.
 - the engine's grouped-GEMM bookkeeping, engine/fast/moe_prefill.py:92-154,509-582 and its
   tile-table test, tests/test_moe_prefill.py:126-146.
+- the post-attention add + RMSNorm, engine/fast/kernels.py:507-523,636-650.
 - the routing tie rule of the engine's kernels, engine/fast/fused.py:553-570,
   engine/fast/prefill_kernels.py:194-219 (descending probability, ties to the lower index).
 
@@ -23,8 +24,9 @@ by the closed-form tile table and stable-permutation invariants; ``batched_mm_ex
 for bit against Transformers' batched_mm_experts_forward; ``sorted_experts`` /
 ``padded_experts`` against each other and Transformers' eager experts loop; ``block_bf16``
 bit for bit against Transformers' Qwen3_5MoeSparseMoeBlock; ``block_fp32`` against a
-float64 restatement; the e4m3 codec against all 256 encodings of torch's cast. Nothing here
-is left parity unpinned.
+float64 restatement; the e4m3 codec against all 256 encodings of torch's cast; ``add_rms``
+bit for bit against Transformers' Qwen3_5MoeRMSNorm, a one-hot closed form, power-of-two
+scale invariance and exact integer sums. Nothing here is left parity unpinned.
 """
 
 from __future__ import annotations
@@ -208,6 +210,18 @@ def pair_outputs_bf16(x, top_i, gate_up, down):
 
 
 # ------------------------------------------------------------------------------- block
+
+
+def add_rms(x, h, weight, eps):
+    """``kernels.add_rms`` (engine/fast/kernels.py:636-650, math of ``_add_rms_kernel``
+    kernels.py:507-523): total = bf16(x + h) (``h`` None: total is x), out =
+    bf16(total * rsqrt(mean(total^2) + eps) * (1 + weight)) in fp32, the zero-centred
+    RMSNorm of Transformers' Qwen3_5MoeRMSNorm (modeling_qwen3_5_moe.py:801-815) and of
+    engine/fast/model.py:75-79. Returns (total, out)."""
+    total = x if h is None else x + h
+    t = total.float()
+    out = t * torch.rsqrt(t.pow(2).mean(-1, keepdim=True) + eps) * (1.0 + weight.float())
+    return total, out.to(x.dtype)
 
 
 def shared_expert(x, sg, su, sd):

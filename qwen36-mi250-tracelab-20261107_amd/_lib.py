@@ -27,6 +27,7 @@ _P = ctypes.c_void_p
 _I = ctypes.c_int
 _LL = ctypes.c_longlong
 _SZ = ctypes.c_size_t
+_F = ctypes.c_float
 
 # name -> (restype, argtypes); every symbol the header declares.
 SIGNATURES: dict[str, tuple] = {
@@ -60,6 +61,12 @@ SIGNATURES: dict[str, tuple] = {
         _I,
         [_P, _I, _I, _I, _I, _I, _I, _P, _I, _P, _P, _P, _P, _I, _P, _P, _P, _P, _I,
          _P, _P, _P, _P, _P, _SZ, _P],
+    ),
+    "moe_add_rmsnorm": (_I, [_P, _P, _P, _I, _I, _F, _P, _P, _P]),
+    "moe_block_forward_add_rms": (
+        _I,
+        [_P, _P, _P, _F, _I, _I, _I, _I, _I, _I, _P, _I, _P, _P, _P, _P, _I, _P, _P, _P, _I,
+         _P, _P, _P, _P, _P, _P, _P, _SZ, _P],
     ),
 }
 

@@ -7,7 +7,8 @@ engine/fast/prefill_kernels.py:676-742): ``mlp`` is a Transformers
 ``shared_expert.{gate,up,down}_proj.weight``, ``shared_expert_gate.weight``,
 ``experts.{gate_up_proj,down_proj}``) and the result is the block's output [T, H].
 ``moe(x, mlp, top_k, residual=r)`` returns ``r + MoE(x)`` rounded as
-``FusedDecode._moe`` (engine/fast/fused.py:887-932).
+``FusedDecode._moe`` (engine/fast/fused.py:887-932). ``add_rms_moe(x, h, w, eps, mlp,
+top_k)`` puts the layer's post-attention add + RMSNorm in front (``moe_block_forward_add_rms``).
 
 Everything runs in one C-ABI call (``moe_block_forward``): router GEMV/GEMM, softmax /
 top-k, count + stable sort + tile table, grouped gate_up (routed experts and the shared
@@ -92,11 +93,51 @@ def moe(x: torch.Tensor, mlp, top_k: int, decode: bool = False,
     """MoE(x) [T, H] bf16 for ``x`` [T, H] (or residual + MoE(x)). With ``return_routing``
     also (top_k_index int64 [T, k], top_k_weights bf16 [T, k], router logits [T, n_pack])."""
     shape = x.shape
-    x2 = x.reshape(-1, shape[-1])
-    _need_cuda(x2)
-    if x2.dtype != torch.bfloat16:
-        raise ValueError(f"x must be bfloat16 (got {x2.dtype})")
-    x2 = x2.contiguous()
+    x2 = _bf16_rows(x, "x")
+    if residual is not None:
+        residual = residual.reshape(x2.shape).to(torch.bfloat16).contiguous()
+    res = _run(x2, mlp, top_k, decode, return_routing, residual=residual)
+    out = res[0].reshape(shape)
+    return (out, *res[1:]) if return_routing else out
+
+
+def add_rms_moe(x: torch.Tensor, h: torch.Tensor | None, norm_weight: torch.Tensor, eps: float,
+                mlp, top_k: int, decode: bool = False, *, return_norm: bool = False,
+                return_routing: bool = False):
+    """``total + MoE(norm)`` with ``(total, norm) = add_rms(x, h, norm_weight, eps)``: the
+    post-attention add + RMSNorm and the MoE block of one decoder layer, as
+    ``x, h = kernels.add_rms(x, h, post_attention_layernorm.weight, eps)`` then the block
+    with ``x`` as its residual (engine/fast/model.py:888-891, fused.py:1074-1076). ``h``
+    None: no add (``total`` is ``x``). On the decode path the norm runs inside the router
+    launch. With ``return_norm`` also (total, norm); with ``return_routing`` also the
+    routing, as ``moe``."""
+    shape = x.shape
+    x2 = _bf16_rows(x, "x")
+    h2 = None if h is None else _bf16_rows(h, "h").reshape(x2.shape)
+    w = norm_weight.reshape(-1)
+    if w.dtype != torch.bfloat16 or w.numel() != x2.shape[1]:
+        raise ValueError(f"norm_weight must be bfloat16 [{x2.shape[1]}]")
+    w = w.contiguous()
+    total = torch.empty_like(x2) if h2 is not None else x2
+    norm = torch.empty_like(x2)
+    res = _run(x2, mlp, top_k, decode, return_routing,
+               norm=(x2, h2, w, float(eps), total if h2 is not None else None, norm))
+    out = res[0].reshape(shape)
+    extra = (total.reshape(shape), norm.reshape(shape)) if return_norm else ()
+    if return_norm or return_routing:
+        return (out, *extra, *res[1:])
+    return out
+
+
+def _bf16_rows(t: torch.Tensor, name: str) -> torch.Tensor:
+    t2 = t.reshape(-1, t.shape[-1])
+    _need_cuda(t2)
+    if t2.dtype != torch.bfloat16:
+        raise ValueError(f"{name} must be bfloat16 (got {t2.dtype})")
+    return t2.contiguous()
+
+
+def _run(x2, mlp, top_k, decode, return_routing, residual=None, norm=None):
     tokens, hidden = x2.shape
     gu, gus, dn, dns, wd = _expert_tensors(mlp.experts)
     experts, two_i, _ = gu.shape
@@ -111,25 +152,27 @@ def moe(x: torch.Tensor, mlp, top_k: int, decode: bool = False,
             raise ValueError(f"{name} weight must be contiguous bfloat16")
     pack = pack_router(mlp)
     n_pack = pack.shape[0]
-    if residual is not None:
-        residual = residual.reshape(tokens, hidden).to(torch.bfloat16).contiguous()
     round_products = decode or tokens <= DECODE_EXPERT_TOKENS
     mode = _lib.ROUND_PRODUCT if round_products else _lib.EXACT_PRODUCT
-    out = torch.empty((tokens, hidden), dtype=torch.bfloat16, device=x2.device)
-    idx = torch.empty((tokens, top_k), dtype=torch.long, device=x2.device) if return_routing else None
-    wts = torch.empty((tokens, top_k), dtype=torch.bfloat16, device=x2.device) if return_routing else None
-    logits = (torch.empty((tokens, n_pack), dtype=torch.bfloat16, device=x2.device)
+    dev = x2.device
+    out = torch.empty((tokens, hidden), dtype=torch.bfloat16, device=dev)
+    idx = torch.empty((tokens, top_k), dtype=torch.long, device=dev) if return_routing else None
+    wts = torch.empty((tokens, top_k), dtype=torch.bfloat16, device=dev) if return_routing else None
+    logits = (torch.empty((tokens, n_pack), dtype=torch.bfloat16, device=dev)
               if return_routing else None)
     if tokens:
         lib = _lib.load()
         nbytes = lib.moe_block_workspace_bytes(tokens, hidden, experts, top_k, inter, inter_s, n_pack)
-        ws = _lib.workspace(x2.device, nbytes)
-        check(lib.moe_block_forward(
-            ptr(x2), tokens, hidden, experts, top_k, inter, inter_s, ptr(pack), n_pack, ptr(gu),
-            ptr(gus), ptr(dn), ptr(dns), wd, ptr(sg), ptr(su), ptr(sd), ptr(residual), mode,
-            ptr(out), ptr(idx), ptr(wts), ptr(logits), ptr(ws), ws.numel(), stream_of(x2)),
-            "moe block")
-    out = out.reshape(shape)
-    if return_routing:
-        return out, idx, wts, logits
-    return out
+        ws = _lib.workspace(dev, nbytes)
+        block_args = (tokens, hidden, experts, top_k, inter, inter_s, ptr(pack), n_pack, ptr(gu),
+                      ptr(gus), ptr(dn), ptr(dns), wd, ptr(sg), ptr(su), ptr(sd))
+        tail = (ptr(out), ptr(idx), ptr(wts), ptr(logits), ptr(ws), ws.numel(), stream_of(x2))
+        if norm is None:
+            check(lib.moe_block_forward(ptr(x2), *block_args, ptr(residual), mode, *tail),
+                  "moe block")
+        else:
+            nx, nh, nw, eps, total, nout = norm
+            check(lib.moe_block_forward_add_rms(
+                ptr(nx), ptr(nh), ptr(nw), eps, *block_args, mode, ptr(total), ptr(nout), *tail),
+                "add_rms + moe block")
+    return out, idx, wts, logits

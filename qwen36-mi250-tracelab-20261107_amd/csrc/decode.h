@@ -29,6 +29,12 @@ struct DecodeArgs {
   uint16_t* act;             // [T * k, I]
   uint16_t* act_sh;          // [T, IS]
   uint16_t* out;             // [T, H]
+  // Optional post-attention add + RMSNorm inside K1 (norm_x non-null): K1 computes
+  // x = RMSNorm(norm_x + norm_h) itself and its workgroup 0 writes norm_sum (when norm_h)
+  // and norm_out, which K2 reads as x and K3 as the residual.
+  const uint16_t *norm_x, *norm_h, *norm_w;
+  float norm_eps;
+  uint16_t *norm_sum, *norm_out;
 };
 
 bool decode_fits(const DecodeArgs& a);

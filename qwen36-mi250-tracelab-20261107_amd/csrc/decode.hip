@@ -10,7 +10,10 @@
 //   K1 k_dec_router   one wave per router row (logits[t, n] = bf16(x_t . Wpack[n])) and one
 //                     wave per shared-expert gate/up row pair (act_sh = SwiGLU). The shared
 //                     expert does not depend on the routing, so its 4 MiB stream overlaps the
-//                     router's HBM round trip instead of following it.
+//                     router's HBM round trip instead of following it. Optionally it
+//                     first computes the layer's post-attention add + RMSNorm of the token
+//                     rows itself (every wave already reads whole rows), which removes that
+//                     launch from a decode layer.
 //   K2 k_dec_gate_up  every workgroup recomputes the softmax / top-k of the T tokens from the
 //                     logits (a few hundred cycles; it replaces the route + sort launch),
 //                     numbers the distinct experts in first-use order, takes one of them and
@@ -28,6 +31,7 @@
 
 #include "moe_common.h"
 #include "route_sort_dev.h"
+#include "add_rms.h"
 #include "decode.h"
 
 namespace moe {
@@ -90,7 +94,9 @@ __device__ __forceinline__ float swiglu(float g, float u) {
 // ------------------------------------------------------------------------------- K1
 
 // grid: n_pack + IS (shared rows, when sh_gate) workgroups of one wave. The weight rows are
-// requested before the token rows so that both are in flight together.
+// requested before the token rows so that both are in flight together. With norm_x every
+// wave normalises the token rows in registers (while its weight rows are in flight) and
+// workgroup 0 stores them.
 template <int NT, int HC>
 __global__ __launch_bounds__(64) void k_dec_router(DecodeArgs a) {
   const int lane = threadIdx.x;
@@ -101,18 +107,48 @@ __global__ __launch_bounds__(64) void k_dec_router(DecodeArgs a) {
   const uint16_t* r0 = router ? a.w_pack + (long long)g * H : a.sh_gate + (long long)n * H;
   const uint16_t* r1 = router ? r0 : a.sh_up + (long long)n * H;
   uint4 w0[HC], w1[HC];
-#pragma unroll
-  for (int c = 0; c < HC; ++c) w0[c] = ld16_stream(r0 + c * 512 + lane * 8);
-  if (!router) {
-#pragma unroll
-    for (int c = 0; c < HC; ++c) w1[c] = ld16_stream(r1 + c * 512 + lane * 8);
-  }
   uint4 xv[NT][HC];
+  if (a.norm_x) {
+    // post-attention add + RMSNorm of each token row, as k_add_rms computes it: the token
+    // rows are requested first, then the weight rows, so the norm's arithmetic runs while
+    // the weight rows are in flight
+    uint4 tot[NT][HC], hv[NT][HC], wv[HC];
+    const bool has_h = a.norm_h != nullptr;
 #pragma unroll
-  for (int t = 0; t < NT; ++t)
+    for (int t = 0; t < NT; ++t) {
+      const long long tr = (long long)min(t, a.T - 1) * H;
+      load_row<HC, true>(a.norm_x + tr, H, lane, tot[t]);
+      if (has_h) load_row<HC, true>(a.norm_h + tr, H, lane, hv[t]);
+    }
+    load_row<HC, true>(a.norm_w, H, lane, wv);
 #pragma unroll
-    for (int c = 0; c < HC; ++c)
-      xv[t][c] = ld16(a.x + (long long)min(t, a.T - 1) * H + c * 512 + lane * 8);
+    for (int c = 0; c < HC; ++c) w0[c] = ld16_stream(r0 + c * 512 + lane * 8);
+    if (!router) {
+#pragma unroll
+      for (int c = 0; c < HC; ++c) w1[c] = ld16_stream(r1 + c * 512 + lane * 8);
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      add_rms_compute<HC>(has_h, H, a.norm_eps, tot[t], hv[t], wv, xv[t]);
+      if (g == 0 && t < a.T) {
+        const long long tr = (long long)t * H;
+        if (has_h) store_row<HC>(a.norm_sum + tr, H, lane, tot[t]);
+        store_row<HC>(a.norm_out + tr, H, lane, xv[t]);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int c = 0; c < HC; ++c) w0[c] = ld16_stream(r0 + c * 512 + lane * 8);
+    if (!router) {
+#pragma unroll
+      for (int c = 0; c < HC; ++c) w1[c] = ld16_stream(r1 + c * 512 + lane * 8);
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int c = 0; c < HC; ++c)
+        xv[t][c] = ld16(a.x + (long long)min(t, a.T - 1) * H + c * 512 + lane * 8);
+  }
   if (router) {
 #pragma unroll
     for (int t = 0; t < NT; ++t) {

@@ -1,6 +1,7 @@
 // extern "C" entry points of libmoe_mi355x.so (declared in include/moe_mi355x.h).
 // Validation, workspace carving and the launch sequence of the MoE block; the kernels
-// live in route_sort.hip, stream_gemm.hip and combine.hip.
+// live in route_sort.hip, expert_gemm.hip, prefill_gemm.hip, decode.hip, add_rms.hip and
+// combine.hip.
 #include <stdarg.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -10,6 +11,7 @@
 #include <string>
 
 #include "../../include/moe_mi355x.h"
+#include "add_rms.h"
 #include "expert_gemm.h"
 #include "decode.h"
 
@@ -754,12 +756,23 @@ size_t moe_block_workspace_bytes(int T, int H, int E, int k, int I, int IS, int 
   return a > b ? a : b;
 }
 
-int moe_block_forward(const void* x, int T, int H, int E, int k, int I, int IS,
-                      const void* w_pack, int n_pack, const void* gate_up, const float* gu_scale,
-                      const void* down, const float* dn_scale, int wdtype, const void* sh_gate,
-                      const void* sh_up, const void* sh_down, const void* residual, int mode,
-                      void* out, long long* top_k_index, void* top_k_weights, void* logits,
-                      void* workspace, size_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// The post-attention add + RMSNorm in front of the block (moe_block_forward_add_rms).
+struct NormIn {
+  const uint16_t *x, *h, *w;
+  float eps;
+  uint16_t *total, *out;
+};
+
+int block_forward(const void* x, int T, int H, int E, int k, int I, int IS, const void* w_pack,
+                  int n_pack, const void* gate_up, const float* gu_scale, const void* down,
+                  const float* dn_scale, int wdtype, const void* sh_gate, const void* sh_up,
+                  const void* sh_down, const void* residual, int mode, void* out,
+                  long long* top_k_index, void* top_k_weights, void* logits, void* workspace,
+                  size_t workspace_bytes, void* stream, const NormIn* nm) {
   int rc = check_experts_shape(T, H, E, k, I);
   if (rc) return rc;
   CHECK_ARG(IS >= 32 && IS % 32 == 0, "shared intermediate must be a multiple of 32 (got %d)", IS);
@@ -799,11 +812,23 @@ int moe_block_forward(const void* x, int T, int H, int E, int k, int I, int IS,
     d.act = w.act;
     d.act_sh = w.act_sh;
     d.out = static_cast<uint16_t*>(out);
+    if (nm) {  // the router launch normalises; gate_up reads its rows, down adds the sum
+      d.norm_x = nm->x, d.norm_h = nm->h, d.norm_w = nm->w, d.norm_eps = nm->eps;
+      d.norm_sum = nm->total, d.norm_out = nm->out;
+      d.x = nm->out;
+      d.residual = nm->h ? nm->total : nm->x;
+    }
     if (decode_fits(d)) {
       HIP_TRY(launch_decode_router(d, s), "decode router launch");
       HIP_TRY(launch_decode_gate_up(d, s), "decode gate_up launch");
       return hip_check(launch_decode_down(d, s), "decode down launch");
     }
+  }
+  if (nm) {
+    HIP_TRY(launch_add_rms(nm->x, nm->h, nm->w, T, H, nm->eps, nm->total, nm->out, s),
+            "add_rms launch");
+    x = nm->out;
+    residual = nm->h ? nm->total : nm->x;
   }
   // The shared expert depends on x alone: where its projections would run as launches of
   // their own anyway (fp8 routed experts, prefill tiles), they run on the auxiliary stream
@@ -841,6 +866,80 @@ int moe_block_forward(const void* x, int T, int H, int E, int k, int I, int IS,
                                   static_cast<const uint16_t*>(residual),
                                   static_cast<uint16_t*>(out), T, H, mode == MOE_ROUND_PRODUCT, s),
                    "combine launch");
+}
+
+bool overlaps(const void* a, const void* b, size_t bytes) {
+  const char *p = static_cast<const char*>(a), *q = static_cast<const char*>(b);
+  return a && b && p < q + bytes && q < p + bytes;
+}
+
+// The aliasing and alignment rules of the add + RMSNorm entry points.
+int check_norm_args(const void* x, const void* h, const void* w, int T, int H, float eps,
+                    const void* total, const void* norm, const void* out) {
+  CHECK_ARG(T >= 0 && H > 0 && H % 8 == 0 && H <= 512 * kAddRmsMaxChunks,
+            "add_rms: H must be a positive multiple of 8 up to %d (got %d)",
+            512 * kAddRmsMaxChunks, H);
+  CHECK_ARG(x && w && norm && (!h || total), "add_rms: null pointer");
+  CHECK_ARG(eps >= 0.f, "add_rms: eps must be >= 0 (got %g)", (double)eps);
+  const size_t bytes = (size_t)T * H * 2;
+  const void* ins[] = {x, h};
+  const void* outs[] = {h ? total : nullptr, norm, out};
+  for (const void* i : ins)
+    for (const void* o : outs)
+      CHECK_ARG(!overlaps(i, o, bytes), "add_rms: outputs must not overlap the inputs");
+  for (int i = 0; i < 3; ++i)
+    for (int j = i + 1; j < 3; ++j)
+      CHECK_ARG(!overlaps(outs[i], outs[j], bytes), "add_rms: outputs must not overlap");
+  CHECK_ARG(((uintptr_t)x | (uintptr_t)h | (uintptr_t)w | (uintptr_t)(h ? total : nullptr) |
+             (uintptr_t)norm) % 16 == 0,
+            "add_rms: rows must be 16-byte aligned");
+  return MOE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int moe_block_forward(const void* x, int T, int H, int E, int k, int I, int IS,
+                      const void* w_pack, int n_pack, const void* gate_up, const float* gu_scale,
+                      const void* down, const float* dn_scale, int wdtype, const void* sh_gate,
+                      const void* sh_up, const void* sh_down, const void* residual, int mode,
+                      void* out, long long* top_k_index, void* top_k_weights, void* logits,
+                      void* workspace, size_t workspace_bytes, void* stream) {
+  return block_forward(x, T, H, E, k, I, IS, w_pack, n_pack, gate_up, gu_scale, down, dn_scale,
+                       wdtype, sh_gate, sh_up, sh_down, residual, mode, out, top_k_index,
+                       top_k_weights, logits, workspace, workspace_bytes, stream, nullptr);
+}
+
+int moe_add_rmsnorm(const void* x, const void* h, const void* weight, int T, int H, float eps,
+                    void* total, void* out, void* stream) {
+  const int rc = check_norm_args(x, h, weight, T, H, eps, total, out, nullptr);
+  if (rc) return rc;
+  return hip_check(launch_add_rms(static_cast<const uint16_t*>(x),
+                                  static_cast<const uint16_t*>(h),
+                                  static_cast<const uint16_t*>(weight), T, H, eps,
+                                  static_cast<uint16_t*>(total), static_cast<uint16_t*>(out),
+                                  (hipStream_t)stream),
+                   "add_rms launch");
+}
+
+int moe_block_forward_add_rms(const void* x, const void* h, const void* norm_weight, float eps,
+                              int T, int H, int E, int k, int I, int IS, const void* w_pack,
+                              int n_pack, const void* gate_up, const float* gu_scale,
+                              const void* down, const float* dn_scale, int wdtype,
+                              const void* sh_gate, const void* sh_up, const void* sh_down,
+                              int mode, void* total, void* norm, void* out,
+                              long long* top_k_index, void* top_k_weights, void* logits,
+                              void* workspace, size_t workspace_bytes, void* stream) {
+  const int rc = check_norm_args(x, h, norm_weight, T, H, eps, total, norm, out);
+  if (rc) return rc;
+  const NormIn nm{static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(h),
+                  static_cast<const uint16_t*>(norm_weight), eps, static_cast<uint16_t*>(total),
+                  static_cast<uint16_t*>(norm)};
+  return block_forward(norm, T, H, E, k, I, IS, w_pack, n_pack, gate_up, gu_scale, down,
+                       dn_scale, wdtype, sh_gate, sh_up, sh_down, nullptr, mode, out,
+                       top_k_index, top_k_weights, logits, workspace, workspace_bytes, stream,
+                       &nm);
 }
 
 }  // extern "C"

@@ -34,6 +34,15 @@ __device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) {
   return (uint32_t)f2bf_bits(lo) | ((uint32_t)f2bf_bits(hi) << 16);
 }
 
+// Two fp32 -> packed bf16 with gfx950's v_cvt_pk_bf16_f32 (round to nearest even, as
+// f2bf_bits for every non-NaN input): one instruction where f2bf_bits takes several.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_bf2_rne(float lo, float hi) {
+  const f32x2_t v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+}
+
 // torch's sigmoid / silu on a bf16 input evaluate in fp32; the caller rounds.
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
 __device__ __forceinline__ float siluf_(float x) { return x / (1.0f + expf(-x)); }

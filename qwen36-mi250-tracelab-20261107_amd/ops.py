@@ -16,6 +16,7 @@ caching allocator; weights are read in place. Nothing here synchronises with the
   decode_router      router | shared gate_up, T <= 4    (engine/fast/fused.py:745-746, 798-840)
   decode_gate_up     top-k + routed gate_up, T <= 4      (engine/fast/fused.py:554-632)
   decode_down        down + combine + shared, T <= 4     (engine/fast/fused.py:635-692)
+  add_rms            residual add + RMSNorm              (engine/fast/kernels.py:636-650)
 """
 
 from __future__ import annotations
@@ -387,3 +388,23 @@ def decode_down(act: torch.Tensor, tokens: int, top_k: int, down: torch.Tensor,
                                       ptr(act_sh), ptr(logits), n_pack, ptr(residual), mode,
                                       ptr(out), stream_of(act)), "decode_down")
     return out
+
+
+def add_rms(x: torch.Tensor, h: torch.Tensor | None, weight: torch.Tensor, eps: float):
+    """``(x + h, RMSNorm(x + h) * (1 + weight))`` in one launch; ``h`` None skips the add and
+    returns ``x`` as the first value. Same arguments and results as the reference's
+    ``kernels.add_rms`` (engine/fast/kernels.py:636-650): total = bf16(x + h),
+    out = bf16(total * rsqrt(mean(total^2) + eps) * (1 + weight)) with fp32 in between."""
+    _need_cuda(x, h, weight)
+    x2 = _bf16(x, "x").reshape(-1, x.shape[-1])
+    rows, n = x2.shape
+    h2 = None if h is None else _bf16(h, "h").reshape(rows, n)
+    w = _bf16(weight, "weight").reshape(-1)
+    if w.numel() != n:
+        raise ValueError(f"weight must have {n} elements (got {w.numel()})")
+    out = torch.empty_like(x2)
+    total = torch.empty_like(x2) if h2 is not None else x2
+    check(_lib.load().moe_add_rmsnorm(ptr(x2), ptr(h2), ptr(w), rows, n, float(eps),
+                                      ptr(total) if h2 is not None else None, ptr(out),
+                                      stream_of(x2)), "add_rms")
+    return total.reshape(x.shape), out.reshape(x.shape)

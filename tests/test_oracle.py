@@ -282,3 +282,62 @@ def test_zipf_router_distinct_experts():
         _, idx = orc.route(F.linear(x, w), 8)
         ds.append(int(torch.unique(idx).numel()))
     assert all(115 <= d <= 165 for d in ds), ds
+
+
+# ------------------------------------------------------------------- add + RMSNorm
+
+
+@pytest.mark.parametrize("with_h", [True, False])
+def test_add_rms_matches_transformers_rmsnorm(with_h):
+    """The oracle's norm == Transformers' Qwen3_5MoeRMSNorm (zero-centred weight) applied to
+    the bf16 sum, bit for bit."""
+    from transformers.models.qwen3_5_moe.modeling_qwen3_5_moe import Qwen3_5MoeRMSNorm
+
+    H, eps = 512, 1e-6
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(7, H, generator=g).to(BF16)
+    h = torch.randn(7, H, generator=g).to(BF16) if with_h else None
+    norm = Qwen3_5MoeRMSNorm(H, eps=eps).to(BF16)
+    with torch.no_grad():
+        norm.weight.copy_((torch.randn(H, generator=g) * 0.3).to(BF16))
+        total, out = orc.add_rms(x, h, norm.weight, eps)
+        want_total = x + h if with_h else x
+        assert torch.equal(total, want_total)
+        assert torch.equal(out, norm(want_total))
+
+
+def test_add_rms_one_hot_closed_form():
+    """x = a e_i, eps = 0, H = 256: mean(x^2) = a^2 / 256, so out_i = sign(a) 16 (1 + w_i)
+    (rounded to bf16) and every other element is zero. Pins the mean over H (not H - 1),
+    the rsqrt and the 1 + w."""
+    H = 256
+    g = torch.Generator().manual_seed(6)
+    w = (torch.randn(H, generator=g) * 0.5).to(BF16)
+    for i, a in ((0, 4.0), (17, -0.5), (255, 2.0 ** -20)):
+        x = torch.zeros(1, H, dtype=BF16)
+        x[0, i] = a
+        _, out = orc.add_rms(x, None, w, 0.0)
+        want = torch.zeros(1, H)
+        want[0, i] = (1.0 if a > 0 else -1.0) * 16.0 * (1.0 + w[i].float())
+        assert torch.equal(out, want.to(BF16)), (i, a)
+
+
+def test_add_rms_power_of_two_scale_invariance():
+    """With eps = 0 scaling a row by 2^j scales mean(x^2) by 4^j exactly and the rsqrt by
+    2^-j exactly, so the normalised row is unchanged bit for bit."""
+    g = torch.Generator().manual_seed(8)
+    x = torch.randn(5, 1024, generator=g).to(BF16)
+    w = (torch.randn(1024, generator=g) * 0.1).to(BF16)
+    _, base = orc.add_rms(x, None, w, 0.0)
+    for j in (-3, 1, 5):
+        _, out = orc.add_rms((x.float() * 2.0 ** j).to(BF16), None, w, 0.0)
+        assert torch.equal(out, base), j
+
+
+def test_add_rms_sum_rounds_to_nearest_even():
+    """Small integers add exactly; 256 + 1 and 256 + 3 are bf16 ties (spacing 2 at 256) and
+    round to the even mantissa: 256 and 260."""
+    x = torch.tensor([[3.0, -7.0, 100.0, 256.0, 256.0, 0.0, 0.0, 0.0]]).to(BF16)
+    h = torch.tensor([[4.0, 2.0, 27.0, 1.0, 3.0, 0.0, 0.0, 0.0]]).to(BF16)
+    total, _ = orc.add_rms(x, h, torch.zeros(8, dtype=BF16), 1e-6)
+    assert total.float().tolist() == [[7.0, -5.0, 127.0, 256.0, 260.0, 0.0, 0.0, 0.0]]
