@@ -9,13 +9,14 @@ include/moe_mi355x.h):
 - ``block.moe(x, mlp, top_k)``: the whole block, router to combine
   (engine/fast/model.py:1139, engine/fast/prefill_kernels.py:676).
 - ``ops``: the individual operations (route, sort, grouped GEMMs, combine).
-- ``fp8``: per-row fp8-e4m3 expert weights.
+- ``fp8``: per-row fp8-e4m3 expert weights; ``checkpoint``: their on-disk format (quantise a
+  bf16 safetensors snapshot once, load the fp8 layers).
 """
 
-from . import _lib, block, experts, fp8, ops, synth  # noqa: F401
+from . import _lib, block, checkpoint, experts, fp8, ops, synth  # noqa: F401
 from ._lib import MoeLibraryError  # noqa: F401
 from .block import moe, pack_router  # noqa: F401
 from .experts import NAME, experts_forward, register  # noqa: F401
 
-__all__ = ["MoeLibraryError", "NAME", "block", "experts", "experts_forward", "fp8", "moe", "ops",
+__all__ = ["MoeLibraryError", "NAME", "block", "checkpoint", "experts", "experts_forward", "fp8", "moe", "ops",
            "pack_router", "register"]
