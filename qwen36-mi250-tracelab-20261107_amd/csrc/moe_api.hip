@@ -411,10 +411,13 @@ hipError_t launch_router(const void* x, int T, int H, const void* w_pack, int n_
   a.P = 0;
   a.E = 0;
   a.T = T;
-  // Token rows per tile: 16-token tiles (K split over 8 waves) give the most waves for a
-  // handful of tokens; larger batches re-read the 1 MiB weight once per tile, so their
-  // tiles grow with T (measured: 16 up to 64 tokens, 32 up to 1024, 64 above).
-  int bm = T <= 64 ? 16 : (T <= 1024 ? 32 : 64);
+  // Token rows per tile: 16-token tiles with K split over 8 waves for every batch below the
+  // hipBLASLt threshold (measured per call: 6.6 / 6.6 / 7.1 / 10.6 µs at 64 / 100 / 200 /
+  // 255 tokens against 24.9 µs with 32-token tiles). One configuration also keeps each
+  // logit's fp32 summation order independent of the batch size, so a token's routing does
+  // not depend on the tokens batched with it. Without a hipBLASLt plan larger batches use
+  // 32-token tiles up to 1024 tokens and 64 above.
+  int bm = T < kRouterBlasltMinTokens ? 16 : (T <= 1024 ? 32 : 64);
   const char* env_bm = getenv("MOE_ROUTER_BM");
   if (env_bm) bm = atoi(env_bm);
   // prefill-sized batches: the plain GEMM through hipBLASLt when it has a plan
