@@ -17,7 +17,9 @@
 //   K2 k_dec_gate_up  every workgroup recomputes the softmax / top-k of the T tokens from the
 //                     logits (a few hundred cycles; it replaces the route + sort launch),
 //                     numbers the distinct experts in first-use order, takes one of them and
-//                     four gate/up row pairs of it, and writes act[pair, n].
+//                     four gate/up row pairs of it, and writes act[pair, n]. For one token
+//                     the weight rows are requested as soon as the selection has reached the
+//                     workgroup's expert, and the rest of the routing overlaps them.
 //   K3 k_dec_down     one wave per hidden row n: y_p = bf16(act_p . Wd[e_p, n]) for every
 //                     pair, the shared expert's row, and the combine of those values in the
 //                     routing order j, gated shared term and residual, written straight to out.
@@ -225,23 +227,59 @@ __global__ __launch_bounds__(64 * kGuWaves) void k_dec_gate_up(DecodeArgs a) {
   const int slot = bid / nrb;
   const int n = (bid - slot * nrb) * kGuWaves + wave;
 
-  // key: the expert of pair `lane` (lanes < P); distinct: the pairs' experts are known to
-  // differ (one token routed here)
-  int key = 0;
-  bool distinct = false;
+  WFrag<FP8> fg[HC], fu[HC];
+  // this workgroup's gate and up rows n of expert ex, requested
+  auto request = [&](int ex) {
+    const long long b = (long long)ex * 2 * a.I;
+    const void* rg = wrow<FP8>(a.gate_up, b + n, H);
+    const void* ru = wrow<FP8>(a.gate_up, b + a.I + n, H);
+#pragma unroll
+    for (int c = 0; c < HC; ++c) {
+      fg[c] = ldraw<FP8>(rg, c * 512 + lane * 8);
+      fu[c] = ldraw<FP8>(ru, c * 512 + lane * 8);
+    }
+  };
+  int e;                       // this workgroup's expert
+  unsigned long long pmask;    // the pairs routed to it
   if (NT == 1 && a.logits) {
-    // one token: every wave routes it itself (no LDS round trip, no barrier)
+    // One token: its k experts are distinct and slot s takes the s-th selected one, so the
+    // weight rows are requested as soon as selection round s has found it; the remaining
+    // rounds, the softmax and the exactness check run while they are in flight. Where the
+    // exact selection (rows whose p order differs from the logit order) gives another
+    // expert for the slot, the rows are requested again.
+    uint16_t raw[EPL];
+    uint32_t keys[EPL];
+    route_keys<EPL>(a.logits, a.E, lane, raw, keys);
+    const int rounds = min(a.k + 1, a.E);
+    uint32_t m = wave_max_u32(keys[0]);
+    const uint32_t top = m;
+    uint32_t sel = lane == 0 ? m : 0u;
+    for (int j = 1; j <= slot; ++j) {
+      m = route_next<EPL>(keys, m);
+      sel = lane == j ? m : sel;
+    }
+    e = 0xffff - (int)(m & 0xffffu);
+    request(e);
+    for (int j = slot + 1; j < rounds; ++j) {
+      m = route_next<EPL>(keys, m);
+      sel = lane == j ? m : sel;
+    }
     int my_idx;
     float my_w;
-    route_row<EPL>(a.logits, a.E, a.k, lane, my_idx, my_w);
-    key = my_idx;
-    distinct = true;
+    route_finish<EPL>(raw, top, sel, rounds, a.E, a.k, lane, my_idx, my_w);
+    const int e_exact = __builtin_amdgcn_readlane(my_idx, slot);
+    if (e_exact != e) {
+      e = e_exact;
+      request(e);
+    }
+    pmask = __ballot(lane < a.k && my_idx == e);
     if (bid == 0 && wave == 0 && lane < a.k) {
       a.idx32[lane] = my_idx;
       a.wts[lane] = f2bf_bits(my_w);
       if (a.idx64) a.idx64[lane] = my_idx;
     }
   } else {
+    // key: the expert of pair `lane` (lanes < P)
     if (a.logits) {
       if (wave < a.T) {
         int my_idx;
@@ -259,38 +297,27 @@ __global__ __launch_bounds__(64 * kGuWaves) void k_dec_gate_up(DecodeArgs a) {
       }
     } else if (threadIdx.x < P) {
       const long long v = a.ids_in[threadIdx.x];
-      const int e = (int)(v < 0 ? 0 : (v >= a.E ? a.E - 1 : v));
-      s_idx[threadIdx.x] = e;
-      if (bid == 0) a.idx32[threadIdx.x] = e;
+      const int ev = (int)(v < 0 ? 0 : (v >= a.E ? a.E - 1 : v));
+      s_idx[threadIdx.x] = ev;
+      if (bid == 0) a.idx32[threadIdx.x] = ev;
     }
     __syncthreads();
-    key = lane < P ? s_idx[lane] : -1;
-  }
-
-  // distinct experts numbered in first-use order (pair order)
-  bool first = lane < P;
-  if (!distinct) {
+    const int key = lane < P ? s_idx[lane] : -1;
+    // distinct experts numbered in first-use order (pair order)
+    bool first = lane < P;
     for (int q = 0; q < P; ++q) {
       const int kq = __builtin_amdgcn_readlane(key, q);
       if (q < lane && kq == key) first = false;
     }
+    const unsigned long long fmask = __ballot(first);
+    const int rank = __popcll(fmask & ((1ull << lane) - 1ull));
+    if (slot >= __popcll(fmask)) return;
+    const unsigned long long smask = __ballot(first && rank == slot);
+    e = __builtin_amdgcn_readlane(key, __ffsll((long long)smask) - 1);
+    pmask = __ballot(lane < P && key == e);
+    request(e);
   }
-  const unsigned long long fmask = __ballot(first);
-  const int rank = __popcll(fmask & ((1ull << lane) - 1ull));
-  if (slot >= __popcll(fmask)) return;
-  const unsigned long long smask = __ballot(first && rank == slot);
-  const int e = __builtin_amdgcn_readlane(key, __ffsll((long long)smask) - 1);
-  unsigned long long pmask = __ballot(lane < P && key == e);  // pairs of this expert
-
   const long long base = (long long)e * 2 * a.I;
-  const void* rg = wrow<FP8>(a.gate_up, base + n, H);
-  const void* ru = wrow<FP8>(a.gate_up, base + a.I + n, H);
-  WFrag<FP8> fg[HC], fu[HC];
-#pragma unroll
-  for (int c = 0; c < HC; ++c) {
-    fg[c] = ldraw<FP8>(rg, c * 512 + lane * 8);
-    fu[c] = ldraw<FP8>(ru, c * 512 + lane * 8);
-  }
   float sg[NT], su[NT];
 #pragma unroll
   for (int t = 0; t < NT; ++t) sg[t] = su[t] = 0.f;

@@ -166,14 +166,14 @@ __device__ __forceinline__ uint32_t bf16_from_order_key(uint32_t k) {
 // and the cases that fail it (p equal for different logits, e.g. exp underflow; a boundary
 // logit under 2^-10 in magnitude or a subnormal boundary p, where fp32 exp need not separate
 // neighbouring logits) take the exact selection on p.
+// Order keys of one row's logits (lane l holds entries l + 64 i, i < EPL), sorted
+// descending per lane: key = (order key of the bf16 logit) << 16 | (0xffff - expert).
 template <int EPL>
-__device__ void route_row(const uint16_t* __restrict__ lrow, int E, int k, int lane,
-                          int& my_idx, float& my_w) {
+__device__ __forceinline__ void route_keys(const uint16_t* __restrict__ lrow, int E, int lane,
+                                           uint16_t (&raw)[EPL], uint32_t (&key)[EPL]) {
   // all EPL loads in flight at once (clamped addresses, masked after)
-  uint16_t raw[EPL];
 #pragma unroll
   for (int i = 0; i < EPL; ++i) raw[i] = lrow[min(lane + kWave * i, E - 1)];
-  uint32_t key[EPL];
 #pragma unroll
   for (int i = 0; i < EPL; ++i) {
     int e = lane + kWave * i;
@@ -187,19 +187,24 @@ __device__ void route_row(const uint16_t* __restrict__ lrow, int E, int k, int l
       key[i - 1] = hi;
       key[i] = lo;
     }
-  // k + 1 rounds: lane j keeps the j-th key (lane k: the first one not selected)
-  const int rounds = min(k + 1, E);
-  uint32_t sel = 0u;
-  uint32_t top = 0u;
-  for (int j = 0; j < rounds; ++j) {
-    const uint32_t m = wave_max_u32(key[0]);
-    if (j == 0) top = m;
-    const bool win = key[0] == m;  // keys are distinct: exactly one lane
+}
+
+// One selection round: the previous round's winner (the lane whose head key is m; keys
+// are distinct) drops its head key; returns the new wave maximum.
+template <int EPL>
+__device__ __forceinline__ uint32_t route_next(uint32_t (&key)[EPL], uint32_t m) {
+  const bool win = key[0] == m;
 #pragma unroll
-    for (int i = 0; i + 1 < EPL; ++i) key[i] = win ? key[i + 1] : key[i];
-    if (win) key[EPL - 1] = 0u;
-    if (lane == j) sel = m;
-  }
+  for (int i = 0; i + 1 < EPL; ++i) key[i] = win ? key[i + 1] : key[i];
+  key[EPL - 1] = win ? 0u : key[EPL - 1];
+  return wave_max_u32(key[0]);
+}
+
+// Softmax over the row and the selected entries' weights, from the first round's maximum
+// (top) and the selected keys (lane j < rounds holds the j-th), with the exact-p fallback.
+template <int EPL>
+__device__ void route_finish(const uint16_t (&raw)[EPL], uint32_t top, uint32_t sel, int rounds,
+                             int E, int k, int lane, int& my_idx, float& my_w) {
   const float mz = bf_bits2f(bf16_from_order_key(top >> 16));
   float p[EPL];
   float s = 0.f;
@@ -237,6 +242,24 @@ __device__ void route_row(const uint16_t* __restrict__ lrow, int E, int k, int l
   }
   my_idx = mine_i;
   my_w = mine_p / tot;
+}
+
+template <int EPL>
+__device__ void route_row(const uint16_t* __restrict__ lrow, int E, int k, int lane,
+                          int& my_idx, float& my_w) {
+  uint16_t raw[EPL];
+  uint32_t key[EPL];
+  route_keys<EPL>(lrow, E, lane, raw, key);
+  // k + 1 rounds: lane j keeps the j-th key (lane k: the first one not selected)
+  const int rounds = min(k + 1, E);
+  uint32_t m = wave_max_u32(key[0]);
+  const uint32_t top = m;
+  uint32_t sel = lane == 0 ? m : 0u;
+  for (int j = 1; j < rounds; ++j) {
+    m = route_next<EPL>(key, m);
+    sel = lane == j ? m : sel;
+  }
+  route_finish<EPL>(raw, top, sel, rounds, E, k, lane, my_idx, my_w);
 }
 
 template <int EPL>

@@ -209,3 +209,31 @@ def test_decode_one_token_down_kernels_agree(pkg, dev, layer, fp8):
             os.environ["MOE_DECODE_DOWN"] = old
     torch.cuda.synchronize()
     assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("E,k", [(256, 8), (64, 8), (16, 4)])
+def test_decode_gate_up_hard_routing_rows(pkg, dev, E, k):
+    """One token per call on rows built to need the exact-selection fallback (p ties from
+    exp underflow, subnormal boundary p, tiny boundary logits, exact logit ties) and the
+    reference's tie families: indices bit-exact against the oracle, weights within one bf16
+    ulp, and the activations bit-equal to the same launch given those indices."""
+    from tests.test_gpu_parity import _hard_rows
+    from tests.helpers import router_rows
+
+    g = torch.Generator().manual_seed(E * 3 + k)
+    rows = torch.cat([_hard_rows(E, g), router_rows(8, E, 11)])
+    H, I = 512, 512
+    gd = torch.Generator(device=dev).manual_seed(E)
+    gu = (torch.randn(E, 2 * I, H, generator=gd, device=dev) * 0.05).to(BF16)
+    for r in range(rows.shape[0]):
+        x = torch.randn(1, H, generator=g).to(BF16).to(dev)
+        lg = rows[r : r + 1].to(dev)
+        act, idx32, wts, idx64 = pkg.ops.decode_gate_up(x, gu, k, logits=lg, experts=E)
+        act2, _, _, _ = pkg.ops.decode_gate_up(x, gu, k, top_k_index=idx64)
+        torch.cuda.synchronize()
+        ref_w, ref_i = orc.route(rows[r : r + 1], k)
+        assert torch.equal(idx64.cpu(), ref_i), f"row {r}"
+        assert torch.equal(idx32.long().cpu(), ref_i)
+        d = (wts.float().cpu() - ref_w.float()).abs()
+        assert (d <= ref_w.float().abs() * 2.0 ** -7 + 1e-30).all(), f"row {r}"
+        assert torch.equal(act, act2), f"row {r}"
