@@ -368,7 +368,7 @@ def pmc_summary(fetch_dir, write_dir, copy_mib, config):
             continue
         fv = sum(fetch[k]) / len(fetch[k]) * 1024.0 * f_fac
         wv = sum(write.get(k, [0.0])) / max(1, len(write.get(k, []))) * 1024.0 * w_fac
-        short = k.replace("void ", "").split("(")[0]
+        short = k.replace("void ", "").replace("(anonymous namespace)::", "").split("(")[0]
         data[f"{config}:{short}"] = {"kernel": short, "fetch_bytes": fv, "write_bytes": wv,
                                       "hbm_bytes_per_launch": int(fv + wv),
                                       "command": cmd_base.format("FETCH_SIZE|WRITE_SIZE")}
