@@ -379,6 +379,8 @@ def pmc_summary(fetch_dir, write_dir, copy_mib, config):
         prev = json.loads(TRAFFIC_FILE.read_text())
     except (OSError, ValueError):
         pass
+    # this config's kernels are replaced, not merged (kernels since removed drop out)
+    prev = {k: v for k, v in prev.items() if not k.startswith(f"{config}:")}
     prev.update(data)
     TRAFFIC_FILE.parent.mkdir(exist_ok=True)
     TRAFFIC_FILE.write_text(json.dumps(prev, indent=1, sort_keys=True) + "\n")
