@@ -11,12 +11,13 @@ include/moe_mi355x.h):
 - ``ops``: the individual operations (route, sort, grouped GEMMs, combine).
 - ``fp8``: per-row fp8-e4m3 expert weights; ``checkpoint``: their on-disk format (quantise a
   bf16 safetensors snapshot once, load the fp8 layers).
+- ``graphs.MoeGraphs``: the block captured once per decode bucket and replayed.
 """
 
-from . import _lib, block, checkpoint, experts, fp8, ops, synth  # noqa: F401
+from . import _lib, block, checkpoint, experts, fp8, graphs, ops, synth  # noqa: F401
 from ._lib import MoeLibraryError  # noqa: F401
 from .block import moe, pack_router  # noqa: F401
 from .experts import NAME, experts_forward, register  # noqa: F401
 
-__all__ = ["MoeLibraryError", "NAME", "block", "checkpoint", "experts", "experts_forward", "fp8", "moe", "ops",
+__all__ = ["MoeLibraryError", "NAME", "block", "checkpoint", "experts", "graphs", "experts_forward", "fp8", "moe", "ops",
            "pack_router", "register"]
