@@ -45,6 +45,9 @@ struct GemmArgs {
 // Launches k_expert_gemm over max_tiles tiles of at most bm (16, 32, 64 or 128) sorted rows.
 // Both operands of one launch must have the same weight type.
 // hipErrorInvalidValue: no kernel configuration fits the operands' shapes.
+// Whether a launch may mix fp8 routed tiles with bf16 shared-expert tiles (MOE_MIXED=0: no;
+// then the caller splits them into two launches).
+bool mixed_enabled();
 hipError_t launch_expert_gemm(int mode, int role, int bm, const GemmArgs& a, int max_tiles,
                               hipStream_t st);
 

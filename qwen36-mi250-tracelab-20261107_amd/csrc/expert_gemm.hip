@@ -39,10 +39,11 @@
 namespace moe {
 
 // KC: K elements per chunk (128; 32 for small test shapes, bf16 only); R: chunks in flight.
-template <int MODE, int WR, int WK, int TOKB, bool HAS_FP8, int KC, int R = 4>
-__global__ __launch_bounds__(64 * WR * WK)
-__attribute__((amdgpu_waves_per_eu(TOKB <= 2 && KC >= 64 ? 3 : 1)))
-void k_expert_gemm(GemmArgs args) {
+// One workgroup's tile (expert e, sorted rows [r0, r1), weight-row block rb) with weights of
+// one type: HAS_FP8 here means the operand's weights are e4m3.
+template <int MODE, int WR, int WK, int TOKB, bool HAS_FP8, int KC, int R>
+__device__ __forceinline__ void gemm_tile(const GemmArgs& args, uint4* __restrict__ lds, int e,
+                                          int r0, int r1, int rb) {
   constexpr int kRowU4 = KC / 8;        // uint4 per staged token-row chunk (bf16)
   // LDS row pitch in uint4: +2 for 128-byte rows, +1 for longer ones (measured fastest)
   constexpr int kPitchU4 = kRowU4 + (kRowU4 == 8 ? 2 : 1);
@@ -57,25 +58,6 @@ void k_expert_gemm(GemmArgs args) {
   constexpr int STG = (TOKB * 16) / (RPI * WR);  // staging instructions per wave per chunk
   static_assert(STG >= 1 && STG * RPI * WR == TOKB * 16, "staging split");
   constexpr int kBufU4 = TOKB * 16 * kPitchU4;  // one chunk of one K slice
-  // LDS: [WK][2 buffers][TOKB*16 rows][pitch] uint4; reused for the K-split reduction.
-  __shared__ uint4 lds[WK * 2 * kBufU4];
-
-  const int nrb = args.nrb;
-  const int tile = blockIdx.x / nrb;
-  const int rb = blockIdx.x - tile * nrb;
-
-  int e, r0, r1;
-  if (args.table) {
-    if (tile >= args.table[3 * args.MT]) return;
-    e = args.table[tile];
-    r0 = args.table[args.MT + tile];
-    r1 = args.table[2 * args.MT + tile];
-  } else {
-    e = args.E;
-    r0 = args.P + tile * BM;
-    if (r0 >= args.P + args.T) return;
-    r1 = min(r0 + BM, args.P + args.T);
-  }
   const bool routed = e < args.E;
   const GemmOperand& op = routed ? args.op[0] : args.op[1];
   if (rb * kOutRowsPerWG >= op.N) return;
@@ -90,7 +72,7 @@ void k_expert_gemm(GemmArgs args) {
   const int kbeg = wk * Kw;
   const int nch = Kw / KC;
   const int ntb = (r1 - r0 + 15) >> 4;
-  constexpr bool use_fp8 = HAS_FP8;  // a launch is all-fp8 or all-bf16
+  constexpr bool use_fp8 = HAS_FP8;
 
   // ---- A operand: this lane's weight row, first NA chunks requested at once.
   long long wrow_off;
@@ -302,6 +284,48 @@ void k_expert_gemm(GemmArgs args) {
   }
 }
 
+// The kernel: looks up its tile and runs it with the tile's weight type. An fp8 launch may
+// also hold bf16 tiles (the shared expert beside fp8 routed experts): those run with half
+// the chunk length, which gives them the fp8 tiles' ring of A registers.
+template <int MODE, int WR, int WK, int TOKB, bool HAS_FP8, int KC, int R = 4>
+__global__ __launch_bounds__(64 * WR * WK)
+__attribute__((amdgpu_waves_per_eu(TOKB <= 2 && KC >= 64 ? 3 : 1)))
+void k_expert_gemm(GemmArgs args) {
+  constexpr int kRowU4 = KC / 8;
+  constexpr int kPitchU4 = kRowU4 + (kRowU4 == 8 ? 2 : 1);
+  constexpr int kBufU4 = TOKB * 16 * kPitchU4;
+  constexpr int BM = 16 * TOKB;
+  // LDS: [WK][2 buffers][TOKB*16 rows][pitch] uint4 at this KC (the larger of the two
+  // bodies'); reused for the K-split reduction.
+  __shared__ uint4 lds[WK * 2 * kBufU4];
+
+
+  const int nrb = args.nrb;
+  const int tile = blockIdx.x / nrb;
+  const int rb = blockIdx.x - tile * nrb;
+
+  int e, r0, r1;
+  if (args.table) {
+    if (tile >= args.table[3 * args.MT]) return;
+    e = args.table[tile];
+    r0 = args.table[args.MT + tile];
+    r1 = args.table[2 * args.MT + tile];
+  } else {
+    e = args.E;
+    r0 = args.P + tile * BM;
+    if (r0 >= args.P + args.T) return;
+    r1 = min(r0 + BM, args.P + args.T);
+  }
+  if constexpr (HAS_FP8) {
+    if ((e < args.E ? args.op[0] : args.op[1]).fp8)
+      gemm_tile<MODE, WR, WK, TOKB, true, KC, R>(args, lds, e, r0, r1, rb);
+    else
+      gemm_tile<MODE, WR, WK, TOKB, false, KC / 2, R>(args, lds, e, r0, r1, rb);
+  } else {
+    gemm_tile<MODE, WR, WK, TOKB, false, KC, R>(args, lds, e, r0, r1, rb);
+  }
+}
+
 // ------------------------------------------------------------------------ dispatch
 
 namespace {
@@ -385,12 +409,19 @@ bool env_cfg(int role, Cfg* out) {
 
 }  // namespace
 
+bool mixed_enabled() {
+  const char* env = getenv("MOE_MIXED");
+  return !(env && env[0] == '0');
+}
+
 hipError_t launch_expert_gemm(int mode, int role, int bm, const GemmArgs& a_in, int max_tiles,
                               hipStream_t st) {
   GemmArgs a = a_in;
   const bool fp8 = (a.op[0].N > 0 && a.op[0].fp8) || (a.op[1].N > 0 && a.op[1].fp8);
-  if (a.op[0].N > 0 && a.op[1].N > 0 && a.op[0].fp8 != a.op[1].fp8)
-    return hipErrorInvalidValue;  // one weight type per launch (the caller splits)
+  // an fp8 launch may hold bf16 tiles (they run at half the chunk length); a launch of
+  // bf16 configurations cannot hold fp8 tiles
+  if (a.op[0].N > 0 && a.op[1].N > 0 && a.op[0].fp8 != a.op[1].fp8 && !mixed_enabled())
+    return hipErrorInvalidValue;
   const int tokb = bm / 16;
   if (bm % 16 || (tokb != 1 && tokb != 2 && tokb != 4 && tokb != 8)) return hipErrorInvalidValue;
   // Preferences: with one 16-token block per tile, split K over 4 waves (more waves for the

@@ -99,7 +99,9 @@ bool block_side_enabled(int T, bool fp8, int bm) {
   const char* env = getenv("MOE_BLOCK_SIDE");
   if (env) return env[0] == '1';
   (void)T;
-  return fp8 || bm == prefill_tile_rows();
+  // fp8 routed experts: the shared expert's bf16 tiles share the routed launches
+  // (mixed_enabled) unless MOE_MIXED=0, which splits them onto the auxiliary stream
+  return (fp8 && !mixed_enabled()) || bm == prefill_tile_rows();
 }
 
 // Decode block: the shared expert's gate/up rows go to the gate_up launch, where they stream
@@ -244,11 +246,11 @@ hipError_t launch_prefill_split(int mode, const GemmArgs& a, int MT, hipStream_t
   return e;
 }
 
-// A launch whose routed experts are fp8 and shared expert bf16 runs as two launches (each
-// kernel is compiled for one weight type); the shared one goes to the auxiliary stream so
-// the two overlap.
+// A launch whose routed experts are fp8 and shared expert bf16 runs as one launch whose
+// bf16 tiles take the kernel's bf16 body (mixed_enabled), or with MOE_MIXED=0 as two
+// launches, the shared one on the auxiliary stream so that the two overlap.
 hipError_t launch_split(int mode, int role, int bm, const GemmArgs& a, int MT, hipStream_t s) {
-  if (a.op[0].N <= 0 || a.op[1].N <= 0 || a.op[0].fp8 == a.op[1].fp8)
+  if (a.op[0].N <= 0 || a.op[1].N <= 0 || a.op[0].fp8 == a.op[1].fp8 || mixed_enabled())
     return launch_expert_gemm(mode, role, bm, a, MT, s);
   GemmArgs v = a;
   v.op[0] = v.op[1];
