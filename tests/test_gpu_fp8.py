@@ -100,3 +100,44 @@ def test_fp8_block_full_shape(pkg, dev, T):
     assert torch.isfinite(out.float()).all()
     assert max_abs(out, f32_q) <= 2e-2 and mean_rel(out, f32_q) <= 6e-3
     assert max_abs(out, f32_m) <= 5e-2 and mean_rel(out, f32_m) <= 6e-2
+
+
+@pytest.mark.parametrize("T", [17, 32])
+def test_fp8_mixed_launch_matches_side_branch(pkg, dev, T):
+    """fp8 routed experts with the bf16 shared expert: one launch holding both tile types
+    (the default) against the shared expert's own launches on the side stream
+    (MOE_MIXED=0). Routing is the same bits; the outputs differ only by the shared
+    projections' fp32 summation order (the split launch's bf16 configuration splits K)."""
+    import os
+
+    import __graft_entry__
+
+    Hh, E, I = 2048, 256, 512
+    gen = torch.Generator(device=dev).manual_seed(12)
+
+    def rnd(*shape):
+        return (torch.randn(*shape, generator=gen, device=dev) * 0.02).to(BF16)
+
+    w = {"router": rnd(E, Hh), "gate_up": rnd(E, 2 * I, Hh), "down": rnd(E, Hh, I),
+         "sh_gate": rnd(I, Hh), "sh_up": rnd(I, Hh), "sh_down": rnd(Hh, I), "sh_gate_w": rnd(1, Hh)}
+    mlp = __graft_entry__._mlp_from_weights(w, dev)
+    q, s = pkg.fp8.quantize_rows(w["gate_up"])
+    q2, s2 = pkg.fp8.quantize_rows(w["down"])
+    mlp.experts.gate_up_proj, mlp.experts.gate_up_scale = q, s
+    mlp.experts.down_proj, mlp.experts.down_scale = q2, s2
+    x = torch.randn(T, Hh, generator=torch.Generator().manual_seed(T)).to(BF16).to(dev)
+    a, ia, wa, _ = pkg.block.moe(x, mlp, 8, return_routing=True)
+    old = os.environ.get("MOE_MIXED")
+    os.environ["MOE_MIXED"] = "0"
+    try:
+        b, ib, wb, _ = pkg.block.moe(x, mlp, 8, return_routing=True)
+    finally:
+        if old is None:
+            os.environ.pop("MOE_MIXED", None)
+        else:
+            os.environ["MOE_MIXED"] = old
+    torch.cuda.synchronize()
+    assert torch.equal(ia, ib) and torch.equal(wa, wb)
+    scale = max(1.0, b.float().abs().max().item())
+    print(f"fp8 mixed vs side branch T={T}: max {max_abs(a, b):.3g}", flush=True)
+    assert max_abs(a, b) <= 4e-3 * scale
