@@ -49,6 +49,9 @@ extern "C" {
 #define MOE_ROUND_PRODUCT 1
 #define MOE_EXACT_PRODUCT 2
 
+/* Version of this interface; raised whenever an entry point's signature changes
+ * (2: moe_decode_gate_up takes the shared expert's rows; add + RMSNorm entry points). */
+#define MOE_ABI_VERSION 2
 int moe_abi_version(void);
 const char* moe_last_error(void);
 

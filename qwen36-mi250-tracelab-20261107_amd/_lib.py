@@ -15,6 +15,7 @@ import torch  # noqa: F401  (loads the HIP runtime the library links against)
 
 LIB_PATH = Path(os.environ.get("MOE_MI355X_LIB", Path(__file__).resolve().parent / "libmoe_mi355x.so"))
 
+ABI_VERSION = 2  # MOE_ABI_VERSION of include/moe_mi355x.h that SIGNATURES describes
 MOE_OK = 0
 MOE_EINVAL = 1
 MOE_EHIP = 2
@@ -95,6 +96,11 @@ def load() -> ctypes.CDLL:
         fn = getattr(lib, name)
         fn.restype = res
         fn.argtypes = args
+    if lib.moe_abi_version() != ABI_VERSION:
+        raise MoeLibraryError(
+            f"{LIB_PATH} implements ABI {lib.moe_abi_version()}, this binding ABI {ABI_VERSION}: "
+            "rebuild it"
+        )
     _lib = lib
     return lib
 

@@ -376,7 +376,7 @@ int run_down(const void* act, int T, int H, int E, int k, int I, const void* dow
 
 extern "C" {
 
-int moe_abi_version(void) { return 1; }
+int moe_abi_version(void) { return MOE_ABI_VERSION; }
 
 const char* moe_last_error(void) { return g_err.c_str(); }
 

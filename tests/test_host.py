@@ -32,7 +32,7 @@ def test_library_exports_every_declared_symbol(pkg):
         assert hasattr(lib, name), name
         assert name in pkg._lib.SIGNATURES, f"{name} has no ctypes signature"
     assert set(pkg._lib.SIGNATURES) == set(_declared_symbols())
-    assert lib.moe_abi_version() == 1
+    assert lib.moe_abi_version() == pkg._lib.ABI_VERSION == 2
 
 
 @pytest.mark.parametrize("T,k,E,bm,sh", [(1, 8, 256, 64, 1), (64, 8, 256, 64, 1),
