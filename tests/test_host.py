@@ -100,3 +100,31 @@ def test_decode_fits_predicate(pkg):
     assert not fits(1, 2048, 256, 8, 512, 768)
     assert not fits(1, 2048, 1024, 8, 512, 512)
     assert not fits(4, 2048, 256, 17, 512, 512)
+
+
+def test_add_rms_argument_checks_before_any_launch(pkg):
+    """moe_add_rmsnorm / moe_block_forward_add_rms reject bad shapes, missing buffers,
+    aliasing and misalignment with MOE_EINVAL before touching the device (the addresses
+    here are never dereferenced)."""
+    lib = pkg._lib.load()
+    EINVAL = pkg._lib.MOE_EINVAL
+    X, Hh, W, TOT, OUT = 0x10000, 0x20000, 0x30000, 0x40000, 0x50000
+    T, H = 2, 64
+    assert lib.moe_add_rmsnorm(X, None, W, T, 60, 1e-6, None, OUT, None) == EINVAL  # H % 8
+    assert lib.moe_add_rmsnorm(X, None, W, T, 8192 + 8, 1e-6, None, OUT, None) == EINVAL
+    assert lib.moe_add_rmsnorm(X, Hh, W, T, H, 1e-6, None, OUT, None) == EINVAL  # no total
+    assert lib.moe_add_rmsnorm(X, None, W, T, H, -1.0, None, OUT, None) == EINVAL  # eps
+    assert lib.moe_add_rmsnorm(X, None, W, T, H, 1e-6, None, X + 64, None) == EINVAL  # overlap
+    assert lib.moe_add_rmsnorm(X, Hh, W, T, H, 1e-6, OUT, OUT + 2, None) == EINVAL  # overlap
+    assert lib.moe_add_rmsnorm(X + 2, None, W, T, H, 1e-6, None, OUT, None) == EINVAL  # align
+    assert b"add_rms" in lib.moe_last_error()
+    P = 0x60000
+    ws = 1 << 20
+    args = (T, 2048, 256, 8, 512, 512, P, 272, P, None, P, None, 0, P, P + 2048 * 512 * 2, P,
+            1)
+    # norm output overlapping the block output
+    assert lib.moe_block_forward_add_rms(X, Hh, W, 1e-6, *args, TOT, OUT, OUT, None, None,
+                                         None, P, ws, None) == EINVAL
+    # total overlapping the input
+    assert lib.moe_block_forward_add_rms(X, Hh, W, 1e-6, *args, X, OUT, OUT + (1 << 16), None,
+                                         None, None, P, ws, None) == EINVAL
