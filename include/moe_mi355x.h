@@ -55,7 +55,7 @@ extern "C" {
 int moe_abi_version(void);
 const char* moe_last_error(void);
 
-/* Sorted rows per tile (bm) the fused entry points use for T tokens: 16 up to 16 tokens,
+/* Sorted rows per tile (bm) the fused entry points use for T tokens: 16 up to 4 tokens,
  * 32 up to 512, above that 256 (the prefill tiles: bf16 weights, hidden a multiple of 256,
  * intermediates of 128) or else 64. A table passed to moe_grouped_gate_up /
  * moe_grouped_down must be built with a bm of 16, 32, 64, 128 or 256. */

@@ -284,12 +284,22 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& args, uint4* __restric
   }
 }
 
+// Waves per SIMD the compiler must allow: three for tiles of up to 32 tokens, unless the
+// configuration's rings (A chunks in flight plus staged token rows) need 96 or more VGPRs,
+// where the 168-register cap of three waves made the compiler spill; two then.
+constexpr int gemm_waves_per_eu(int WR, int TOKB, bool fp8, int KC, int R) {
+  const int lpca = fp8 ? KC / 64 : KC / 32;
+  const int stg = (TOKB * 16) / ((64 / (KC / 8)) * WR);
+  const int ring = 4 * R * (lpca + stg);
+  return TOKB <= 2 && KC >= 64 ? (ring >= 96 ? 2 : 3) : 1;
+}
+
 // The kernel: looks up its tile and runs it with the tile's weight type. An fp8 launch may
 // also hold bf16 tiles (the shared expert beside fp8 routed experts): those run with half
 // the chunk length, which gives them the fp8 tiles' ring of A registers.
 template <int MODE, int WR, int WK, int TOKB, bool HAS_FP8, int KC, int R = 4>
 __global__ __launch_bounds__(64 * WR * WK)
-__attribute__((amdgpu_waves_per_eu(TOKB <= 2 && KC >= 64 ? 3 : 1)))
+__attribute__((amdgpu_waves_per_eu(gemm_waves_per_eu(WR, TOKB, HAS_FP8, KC, R))))
 void k_expert_gemm(GemmArgs args) {
   constexpr int kRowU4 = KC / 8;
   constexpr int kPitchU4 = kRowU4 + (kRowU4 == 8 ? 2 : 1);
