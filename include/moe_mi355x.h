@@ -55,7 +55,7 @@ extern "C" {
 int moe_abi_version(void);
 const char* moe_last_error(void);
 
-/* Sorted rows per tile (bm) the fused entry points use for T tokens: 16 up to 4 tokens,
+/* Sorted rows per tile (bm) the fused entry points use for T tokens: 16 for one token,
  * 32 up to 512, above that 256 (the prefill tiles: bf16 weights, hidden a multiple of 256,
  * intermediates of 128) or else 64. A table passed to moe_grouped_gate_up /
  * moe_grouped_down must be built with a bm of 16, 32, 64, 128 or 256. */
@@ -124,8 +124,10 @@ int moe_combine(const void* y, const void* w, int T, int H, int k, const void* y
 
 /* Decode stages (T <= 4 tokens; H a multiple of 512 up to 4096, I and IS 512 or 1024,
  * E <= 512, T*k <= 64): the three launches of engine/fast/fused.py's FusedDecode._moe
- * (fused.py:887-932). moe_decode_fits says whether a shape takes this path; the fused
- * entry points below use it on their own for such shapes (MOE_DECODE=0 turns it off). */
+ * (fused.py:887-932). moe_decode_fits says whether a shape fits this path; the fused
+ * entry points below take it on their own for such shapes with bf16 experts, and with
+ * fp8 experts up to 2 tokens (the tiled path is faster above; MOE_DECODE=0 turns the
+ * decode path off). */
 int moe_decode_fits(int T, int H, int E, int k, int I, int IS);
 
 /* Stage 1: router logits [T, n_pack] (as moe_router_logits) and, with sh_gate / sh_up

@@ -45,10 +45,11 @@ int tile_rows_for(int T, bool fp8 = false, int H = 2048, int I = 512, int IS = 5
     int v = atoi(env);
     if (v == 16 || v == 32 || v == 64 || v == 128 || v == prefill_tile_rows()) return v;
   }
-  // 32-row tiles from 5 tokens: per layer (12 layers cycled) 8 / 16 tokens take 81 / 113 µs
+  // 32-row tiles from 2 tokens: per layer (12 layers cycled) 8 / 16 tokens take 81 / 113 µs
   // with fp8 experts against 128 / 213 with 16-row tiles, and 102 / 150 against 107 / 166
-  // with bf16
-  if (T <= 4) return 16;
+  // with bf16; at 2 / 3 / 4 tokens (16 layers) fp8 50 / 53 / 56 against 55 / 68 / 79 and
+  // bf16 49 / 59 / 69 against 51 / 60 / 69; one token 44 against 40 (bf16)
+  if (T <= 1) return 16;
   if (T <= 512) return 32;
   const bool prefill_ok = !fp8 && H % 256 == 0 && I % 128 == 0 && IS % 128 == 0 &&
                           H % 64 == 0 && I % 64 == 0 && IS % 64 == 0;
@@ -88,6 +89,12 @@ bool decode_enabled() {
   const char* env = getenv("MOE_DECODE");
   return !(env && env[0] == '0');
 }
+
+// Whether the decode kernels take T tokens (given that the shape fits them): measured per
+// layer (16 layers cycled) against the tiled path with 32-row tiles, bf16 decode
+// 17.6 / 31.2 / 52.8 / 67.6 µs at 1 / 2 / 3 / 4 tokens against 43.9 / 49.3 / 58.6 / 68.7,
+// fp8 17.1 / 35.0 / 60.3 / 78.4 against 47.1 / 50.2 / 52.6 / 56.2: fp8 up to 2 tokens.
+bool decode_takes(int T, bool fp8) { return decode_enabled() && T <= (fp8 ? 2 : kDecMaxTokens); }
 
 // Prefill shared-expert tiles on the auxiliary stream unless MOE_PREFILL_SIDE=0.
 bool prefill_side_enabled() {
@@ -685,7 +692,7 @@ int moe_experts_forward(const void* x, int T, int H, int E, int k, int I,
   CHECK_ARG(workspace && workspace_bytes >= w.bytes, "workspace too small: %zu < %zu",
             workspace_bytes, w.bytes);
   hipStream_t s = (hipStream_t)stream;
-  if (decode_enabled()) {
+  if (decode_takes(T, wdtype == MOE_WEIGHTS_FP8_E4M3)) {
     DecodeArgs d{};
     d.x = static_cast<const uint16_t*>(x);
     d.T = T, d.H = H, d.E = E, d.k = k, d.I = I;
@@ -799,7 +806,7 @@ int block_forward(const void* x, int T, int H, int E, int k, int I, int IS, cons
   uint16_t* lg = logits ? static_cast<uint16_t*>(logits) : w.logits;
   long long* i64 = top_k_index ? top_k_index : w.idx64;
   uint16_t* wt = top_k_weights ? static_cast<uint16_t*>(top_k_weights) : w.w;
-  if (decode_enabled()) {
+  if (decode_takes(T, wdtype == MOE_WEIGHTS_FP8_E4M3)) {
     DecodeArgs d{};
     d.x = static_cast<const uint16_t*>(x);
     d.T = T, d.H = H, d.E = E, d.k = k, d.I = I, d.IS = IS;
