@@ -254,6 +254,34 @@ def run_config(torch, dev, name, T, layers, steps, warmup, zipf=False, fp8=False
     return res
 
 
+def small_batches(torch, dev, layers=8, reps=20):
+    """µs per layer of decode steps of 2-16 tokens (bf16 and fp8 experts, ``layers`` layers
+    cycled, graph-replayed): the range between the C2 and C3 / C5 workloads, where the
+    block picks between the decode kernels and the tiled expert GEMM."""
+    pkg = load_pkg()
+    out = {}
+    for fp8 in (False, True):
+        mlps = [make_layer(torch, dev, seed=700 + li, fp8=fp8)[0] for li in range(layers)]
+        for mlp in mlps:
+            pkg.block.pack_router(mlp)
+        for T in (2, 4, 8, 16):
+            g = torch.Generator(device=dev).manual_seed(T)
+            xs = [torch.randn(T, H, generator=g, device=dev).to(torch.bfloat16) for _ in mlps]
+
+            def step():
+                for mlp, x in zip(mlps, xs):
+                    pkg.block.moe(x, mlp, K_TOP, decode=True)
+
+            graph = capture(torch, step)
+            us = time_graph(torch, graph, reps, 4) * 1000.0 / (reps * layers)
+            out[f"{'fp8' if fp8 else 'bf16'}_T{T}"] = round(us, 2)
+            del graph
+        del mlps
+        torch.cuda.empty_cache()
+    log(f"[batches] {json.dumps(out)}")
+    return out
+
+
 def cpu_baseline(torch, seconds):
     """The CPU torch restatement of the reference path (oracle.block_bf16: Transformers
     block with batched_mm experts, engine/experts.py) on C2, timed on this host."""
@@ -394,7 +422,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=32)
-    ap.add_argument("--configs", default="c2,c3,c4,c5")
+    ap.add_argument("--configs", default="c2,c3,c4,c5,batches")
     ap.add_argument("--layers", type=int, default=16)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -444,11 +472,16 @@ def main():
     if "c5" in cfgs:
         results["c5"] = run_config(torch, dev, "c5", 32, 40, max(40, args.steps // 40 * 40),
                                    40, fp8=True)
-    head = results.get("c2") or next(iter(results.values()))
+    if "batches" in cfgs:
+        results["batches"] = small_batches(torch, dev)
+    workloads = {k: v for k, v in results.items() if k != "batches"}
+    if not workloads:
+        raise SystemExit("bench.py: --configs needs at least one of c2, c3, c4, c5")
+    head = workloads.get("c2") or next(iter(workloads.values()))
     cpu = None if args.no_cpu else cpu_baseline(torch, args.cpu_seconds)
     kbytes, kus = head["gate_up_bytes"], head["gate_up_us"]
     achieved = kbytes / (kus * 1e-6) / 1e9
-    traffic = measured_traffic(head["gate_up_kernel"], head_name(results))
+    traffic = measured_traffic(head["gate_up_kernel"], head_name(workloads))
     line = {
         "metric": METRIC,
         "value": head["us_per_layer"],
