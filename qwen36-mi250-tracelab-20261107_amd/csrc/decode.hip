@@ -228,9 +228,14 @@ __global__ __launch_bounds__(64 * kGuWaves) void k_dec_gate_up(DecodeArgs a) {
   const int n = (bid - slot * nrb) * kGuWaves + wave;
 
   WFrag<FP8> fg[HC], fu[HC];
-  // this workgroup's gate and up rows n of expert ex, requested
+  float scg = 1.f, scu = 1.f;  // fp8 row scales, requested with the rows
+  // this workgroup's gate and up rows n of expert ex (and their scales), requested
   auto request = [&](int ex) {
     const long long b = (long long)ex * 2 * a.I;
+    if (a.gu_scale) {
+      scg = a.gu_scale[b + n];
+      scu = a.gu_scale[b + a.I + n];
+    }
     const void* rg = wrow<FP8>(a.gate_up, b + n, H);
     const void* ru = wrow<FP8>(a.gate_up, b + a.I + n, H);
 #pragma unroll
@@ -331,11 +336,6 @@ __global__ __launch_bounds__(64 * kGuWaves) void k_dec_gate_up(DecodeArgs a) {
       su[t] = dot8(wu, xv[t][c], su[t]);
     }
   }
-  float scg = 1.f, scu = 1.f;
-  if (a.gu_scale) {
-    scg = a.gu_scale[base + n];
-    scu = a.gu_scale[base + a.I + n];
-  }
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     sg[t] = wave_sum(sg[t]) * scg;
@@ -402,10 +402,12 @@ __global__ __launch_bounds__(kDecThreads) void k_dec_down(DecodeArgs a) {
     WFrag<FP8> wf[8][IC];
     uint4 av[8][IC];
     int ev[8];
+    float dsc[8];  // fp8 row scales, requested with the rows
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int p = min(p0 + i, P - 1);
       ev[i] = __builtin_amdgcn_readlane(kv, p);
+      dsc[i] = a.dn_scale ? a.dn_scale[(long long)ev[i] * H + n] : 1.f;
       const void* row = wrow<FP8>(a.down, (long long)ev[i] * H + n, I);
 #pragma unroll
       for (int c = 0; c < IC; ++c) {
@@ -421,7 +423,7 @@ __global__ __launch_bounds__(kDecThreads) void k_dec_down(DecodeArgs a) {
 #pragma unroll
       for (int c = 0; c < IC; ++c) s = dot8(decode<FP8>(wf[i][c]), av[i][c], s);
       s = wave_sum(s);
-      if (a.dn_scale) s *= a.dn_scale[(long long)ev[i] * H + n];
+      s *= dsc[i];
       const float y = rbf(s);
       const float w = __shfl(wv, p);
       const float term = a.round_w ? rbf(w * y) : w * y;
@@ -503,16 +505,18 @@ __global__ __launch_bounds__(1024) void k_dec_down1(DecodeArgs a) {
 #pragma unroll
       for (int c = 0; c < IC; ++c) wf[r][c] = ldraw<FP8>(row, c * 512 + lane * 8);
     }
-    float scl = 1.f;
-    const float* sc = a.dn_scale ? a.dn_scale + (long long)e * H + n0 : nullptr;
+    // fp8 row scales requested with the rows, not after the dot products
+    float scl[kDownRows];
+#pragma unroll
+    for (int r = 0; r < kDownRows; ++r)
+      scl[r] = a.dn_scale ? a.dn_scale[(long long)e * H + n0 + r] : 1.f;
 #pragma unroll
     for (int r = 0; r < kDownRows; ++r) {
       float d = 0.f;
 #pragma unroll
       for (int c = 0; c < IC; ++c) d = dot8(decode<FP8>(wf[r][c]), av[c], d);
       d = wave_sum(d);
-      if (sc) scl = sc[r];
-      const float y = rbf(d * scl);
+      const float y = rbf(d * scl[r]);
       if (lane == r) s_term[wave][r] = a.round_w ? rbf(w * y) : w * y;
     }
   }
