@@ -280,6 +280,51 @@ __device__ void route_rows(const uint16_t* __restrict__ logits, long long ld, in
   }
 }
 
+// Two rows of one wave (t1 < 0: none), their key set-up and selection rounds interleaved:
+// the rounds are chains of dependent cross-lane steps, so two independent chains fill each
+// other's wait slots. Each row's result is that of route_rows on it alone.
+template <int EPL>
+__device__ void route_rows2(const uint16_t* __restrict__ logits, long long ld, int t0, int t1,
+                            int E, int k, int lane, long long* __restrict__ idx64,
+                            int* __restrict__ idx32, uint16_t* __restrict__ w_out,
+                            int* __restrict__ keys_lds, int* __restrict__ counts_g) {
+  const int ts[2] = {t0, t1 < 0 ? t0 : t1};
+  uint16_t raw[2][EPL];
+  uint32_t key[2][EPL];
+#pragma unroll
+  for (int r = 0; r < 2; ++r) route_keys<EPL>(logits + (long long)ts[r] * ld, E, lane, raw[r], key[r]);
+  const int rounds = min(k + 1, E);
+  uint32_t m[2], top[2], sel[2];
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    m[r] = wave_max_u32(key[r][0]);
+    top[r] = m[r];
+    sel[r] = lane == 0 ? m[r] : 0u;
+  }
+  for (int j = 1; j < rounds; ++j) {
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      m[r] = route_next<EPL>(key[r], m[r]);
+      sel[r] = lane == j ? m[r] : sel[r];
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    if (r == 1 && t1 < 0) break;
+    int my_i;
+    float my_w;
+    route_finish<EPL>(raw[r], top[r], sel[r], rounds, E, k, lane, my_i, my_w);
+    if (lane < k) {
+      const long long pidx = (long long)ts[r] * k + lane;
+      if (idx64) idx64[pidx] = my_i;
+      if (idx32) idx32[pidx] = my_i;
+      if (w_out) w_out[pidx] = f2bf_bits(my_w);
+      if (keys_lds) keys_lds[pidx] = my_i;
+      if (counts_g) atomicAdd(counts_g + my_i, 1);
+    }
+  }
+}
+
 // ------------------------------------------------------------------ block-level helpers
 
 // Exclusive scan of one int per thread over the whole block (<= 1024 threads).
@@ -387,8 +432,10 @@ __device__ void route_sort_block(const uint16_t* __restrict__ logits, long long 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
   for (int e = threadIdx.x; e < E; e += blockDim.x) L.hist[e] = 0;
   if (logits) {
-    for (int t = wave; t < T; t += nw)
-      route_rows<EPL>(logits, ld, t, E, k, lane, idx64, idx32, w_out, L.keys, nullptr);
+    // two tokens per pass of a wave, interleaved
+    for (int t = wave; t < T; t += 2 * nw)
+      route_rows2<EPL>(logits, ld, t, t + nw < T ? t + nw : -1, E, k, lane, idx64, idx32, w_out,
+                       L.keys, nullptr);
   } else {
     for (int p = threadIdx.x; p < P; p += blockDim.x) {
       long long v = ids64_in ? ids64_in[p] : (long long)ids32_in[p];
