@@ -5,8 +5,9 @@ python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs c2,c3,c4,c5] [--n
 A step is one MoE layer call (router -> top-k -> sort -> grouped gate_up -> grouped down
 -> combine) on one batch of synthetic tokens with that layer's inputs already in HBM.
 Layers cycle through L distinct weight sets (more bytes than L2 + MALL) so every step
-streams its experts from HBM. Steps are captured in a HIP graph of L layer calls and
-replayed; K is rounded up to a multiple of L and the JSON reports the K timed.
+streams its experts from HBM. The W warmup steps and the K timed steps are each captured
+as one HIP graph of exactly that many layer calls (cycling the L layers); the timed region
+is one replay of the K-call graph, bracketed by device synchronisations.
 
 The headline workload is C2 (decode batch 1, H2048 E256 top-8 + shared, I=IS=512, bf16):
 ``value`` = microseconds per layer (lower is better). The same line carries the C3
@@ -92,12 +93,23 @@ def load_pkg():
 
 
 def layer_bytes(D, T, fp8=False):
-    """Algorithmic HBM bytes of one layer: each distinct expert's weights once, the shared
-    expert, the router | shared-gate rows, activations in and out."""
-    per_expert = 3 * I * H * (1 if fp8 else 2) + (3 * I * 4 if fp8 else 0)  # + fp32 row scales
+    """Algorithmic HBM bytes of one layer: each distinct expert's weights once (+ fp32 row
+    scales for fp8), the shared expert, the router | shared-gate rows, the token rows in and
+    the output rows out. Nothing an implementation chooses to write and read back."""
+    per_expert = 3 * I * H * (1 if fp8 else 2) + (3 * I * 4 if fp8 else 0)
     weights = D * per_expert + 3 * IS * H * 2 + (E + 1) * H * 2
-    acts = T * H * 2 * 2 + T * K_TOP * (I + H) * 2 * 2
-    return weights + acts
+    return weights + T * H * 2 * 2
+
+
+def impl_bytes(T, decode):
+    """This implementation's own intermediate round trips per layer (written, then read
+    back): the activations act [T*k, I] and act_sh [T, IS], the router logits, and in the
+    tiled / prefill regimes the pair outputs y [T*k, H] and y_sh [T, H] that the combine
+    reads."""
+    b = (T * K_TOP * I + T * IS) * 2 * 2 + T * 320 * 2 * 2
+    if not decode:
+        b += (T * K_TOP * H + T * H) * 2 * 2
+    return b
 
 
 def gate_up_bytes(D, T, fp8=False, logits=False):
@@ -126,7 +138,10 @@ def capture(torch, fn):
     return g
 
 
-def time_graph(torch, g, reps, warmup):
+def time_graph(torch, g, reps, warmup, pre=None):
+    """ms of ``reps`` replays of ``g`` after ``warmup`` untimed ones (and one of ``pre``)."""
+    if pre is not None:
+        pre.replay()
     for _ in range(warmup):
         g.replay()
     torch.cuda.synchronize()
@@ -138,6 +153,9 @@ def time_graph(torch, g, reps, warmup):
     stop.record()
     torch.cuda.synchronize()
     return start.elapsed_time(stop)  # ms
+
+
+_ACC_SAMPLE: dict = {}
 
 
 def run_config(torch, dev, name, T, layers, steps, warmup, zipf=False, fp8=False):
@@ -165,30 +183,48 @@ def run_config(torch, dev, name, T, layers, steps, warmup, zipf=False, fp8=False
         ok = ok and bool(torch.isfinite(out.float()).all())
     torch.cuda.synchronize()
     D = sum(Ds) / len(Ds)
+    if name == "c2":
+        # the GPU result of layer 0 for the CPU leg's accuracy check (cpu_baseline)
+        mlp, x = mlps[0], xs[0]
+        out, idx, wts, logits = pkg.block.moe(x, mlp, K_TOP, decode=True, return_routing=True)
+        sh = mlp.shared_expert
+        _ACC_SAMPLE.update(
+            x=x.cpu(), out=out.cpu(), idx=idx.cpu(), wts=wts.cpu(), logits=logits.cpu(),
+            w={"router": mlp.gate.weight, "gate_up": mlp.experts.gate_up_proj,
+               "down": mlp.experts.down_proj, "sh_gate": sh.gate_proj.weight,
+               "sh_up": sh.up_proj.weight, "sh_down": sh.down_proj.weight,
+               "sh_gate_w": mlp.shared_expert_gate.weight})
 
-    def layer_pass():
-        for mlp, x in zip(mlps, xs):
-            pkg.block.moe(x, mlp, K_TOP, decode=T <= 64)
+    def calls(n):
+        # n layer calls, cycling the L distinct layers
+        def run():
+            for i in range(n):
+                pkg.block.moe(xs[i % layers], mlps[i % layers], K_TOP, decode=T <= 64)
+        return run
 
-    graph = capture(torch, layer_pass)
+    # exactly `steps` timed layer calls after `warmup` untimed ones, each a graph of its own
+    graph = capture(torch, calls(steps))
+    wgraph = capture(torch, calls(warmup)) if warmup > 0 else None
+    ms = time_graph(torch, graph, 1, 0, pre=wgraph)
+    nsteps = steps
+    us_layer = ms * 1000.0 / nsteps
     reps = max(1, -(-steps // layers))
     wreps = max(1, -(-warmup // layers))
-    ms = time_graph(torch, graph, reps, wreps)
-    nsteps = reps * layers
-    us_layer = ms * 1000.0 / nsteps
     lbytes = sum(layer_bytes(d, T, fp8) for d in Ds) / len(Ds)
     res = {
-        "T": T, "layers": layers, "steps": nsteps, "us_per_layer": round(us_layer, 3),
+        "T": T, "layers": layers, "steps": nsteps, "warmup": warmup,
+        "us_per_layer": round(us_layer, 3),
         "tokens_per_s": round(T / (us_layer * 1e-6), 1), "distinct_experts": round(D, 2),
         "layer_bytes": int(lbytes), "layer_TBps": round(lbytes / (us_layer * 1e-6) / 1e12, 3),
         "layer_hbm_frac": round(lbytes / (us_layer * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+        "impl_bytes": impl_bytes(T, pkg.ops.decode_fits(T, H, E, K_TOP, I, IS)),
         "finite": ok, "weights": "fp8_e4m3" if fp8 else "bf16",
     }
     if T >= 1024:
         flops = 2 * T * K_TOP * 3 * I * H + 2 * T * 3 * IS * H + 2 * T * (E + 1) * H
         res["tflops"] = round(flops / (us_layer * 1e-6) / 1e12, 2)
         res["mfma_frac_bf16"] = round(flops / (us_layer * 1e-6) / 1e12 / BF16_PEAK_TFLOPS, 4)
-    del graph
+    del graph, wgraph
 
     if T <= 4:
         # the decoder layer's post-attention add + RMSNorm in front of the block: fused into
@@ -208,7 +244,7 @@ def run_config(torch, dev, name, T, layers, steps, warmup, zipf=False, fp8=False
 
         for key, fn in (("add_rms_moe_us", fused_pass), ("add_rms_then_moe_us", separate_pass)):
             graph = capture(torch, fn)
-            res[key] = round(time_graph(torch, graph, reps, wreps) * 1000.0 / nsteps, 3)
+            res[key] = round(time_graph(torch, graph, reps, wreps) * 1000.0 / (reps * layers), 3)
             del graph
 
     # the dominant kernel alone, as the block launches it: the decode gate_up (routing in the
@@ -241,7 +277,7 @@ def run_config(torch, dev, name, T, layers, steps, warmup, zipf=False, fp8=False
 
     graph = capture(torch, gate_up_pass)
     ms = time_graph(torch, graph, reps, wreps)
-    us_k = ms * 1000.0 / nsteps
+    us_k = ms * 1000.0 / (reps * layers)
     kbytes = sum(gate_up_bytes(d, T, fp8, logits=decode) for d in Ds) / len(Ds)
     res["gate_up_kernel"] = "k_dec_gate_up" if decode else (
         "k_prefill_gemm" if T > 512 and not fp8 else "k_expert_gemm")
@@ -313,7 +349,27 @@ def cpu_baseline(torch, seconds):
             ts.append(time.perf_counter() - t1)
         ts.sort()
         others[name] = {"T": T, "us_per_layer": round(ts[len(ts) // 2] * 1e6, 1), "calls": len(ts)}
+    acc = None
+    if _ACC_SAMPLE:
+        # the same check the parity tests make, on the bench's own C2 layer 0: the GPU output
+        # and the reference torch path (batched_mm rounding) against the fp32 oracle
+        sm = _ACC_SAMPLE
+        lg = sm["logits"][:, :E].float()
+        f32 = orc.block_fp32(sm["x"], sm["w"], sm["idx"], logits=lg)
+        wc, ic = orc.compact_experts(sm["w"], sm["idx"])
+        ref = orc.block_bf16_routed(sm["x"], wc, ic, sm["wts"], sm["logits"][:, E:E + 1],
+                                    decode=True)
+
+        def mrel(a, b):
+            return float((a.float() - b).abs().mean() / b.abs().mean())
+
+        acc = {"max_abs_vs_fp32": round(float((sm["out"].float() - f32).abs().max()), 6),
+               "mean_rel_vs_fp32": round(mrel(sm["out"], f32), 6),
+               "mean_rel_ref_path_vs_fp32": round(mrel(ref, f32), 6),
+               "bar": "max-abs 2e-2; mean-rel 5e-3, or 1.1x the reference path's own "
+                      "mean-rel where that exceeds 5e-3 (its bf16 rounding points alone do)"}
     return {
+        "accuracy_c2": acc,
         "value": round(med * 1e6, 1), "unit": "us/layer", "cores": torch.get_num_threads(),
         "affinity_cores": len(os.sched_getaffinity(0)), "kind": "port",
         "sample": f"C2 decode batch 1, {n} layer calls of the bf16 CPU torch path "
@@ -479,6 +535,7 @@ def main():
         raise SystemExit("bench.py: --configs needs at least one of c2, c3, c4, c5")
     head = workloads.get("c2") or next(iter(workloads.values()))
     cpu = None if args.no_cpu else cpu_baseline(torch, args.cpu_seconds)
+    accuracy = cpu.pop("accuracy_c2", None) if cpu else None
     kbytes, kus = head["gate_up_bytes"], head["gate_up_us"]
     achieved = kbytes / (kus * 1e-6) / 1e9
     traffic = measured_traffic(head["gate_up_kernel"], head_name(workloads))
@@ -488,7 +545,7 @@ def main():
         "unit": "us/layer",
         "n_gpus": 1,
         "steps": head["steps"],
-        "warmup": args.warmup,
+        "warmup": head["warmup"],
         "ms_per_step": round(head["us_per_layer"] / 1000.0, 6),
         "higher_is_better": False,
         "scaling": "weak",
@@ -508,6 +565,7 @@ def main():
                      "traffic_source": traffic["source"] if traffic else None,
                      "bytes_per_launch": kbytes, "us_per_launch": kus},
         "cpu_baseline": cpu,
+        "accuracy_c2": accuracy,
         "configs": results,
     }
     print(json.dumps(line), flush=True)

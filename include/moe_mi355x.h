@@ -3,9 +3,8 @@
  * Plain device pointers, sizes and a hipStream_t passed as void*. No entry point
  * allocates device memory or synchronises with the host: callers pass a workspace of
  * moe_*_workspace_bytes(...) bytes, so every call can be captured in a HIP graph.
- * Workspace contract: its first MOE_SYNC_BYTES bytes hold arrival counters of the fused
- * kernel tails; they must be zero before the first call that uses the workspace, and
- * every call leaves them zero. Calls that share a workspace must not overlap (use one
+ * Workspace contract: scratch only; its contents need no initialisation and are
+ * meaningless between calls. Calls that share a workspace must not overlap (use one
  * workspace per stream).
  * All tensors are contiguous row-major. bf16 tensors are passed as raw 16-bit words.
  * fp8 weights are OCP e4m3fn bytes with one fp32 scale per output row.
@@ -30,8 +29,6 @@
 extern "C" {
 #endif
 
-#define MOE_SYNC_BYTES 4096
-
 #define MOE_OK 0
 #define MOE_EINVAL 1
 #define MOE_EHIP 2
@@ -49,9 +46,10 @@ extern "C" {
 #define MOE_ROUND_PRODUCT 1
 #define MOE_EXACT_PRODUCT 2
 
-/* Version of this interface; raised whenever an entry point's signature changes
- * (2: moe_decode_gate_up takes the shared expert's rows; add + RMSNorm entry points). */
-#define MOE_ABI_VERSION 2
+/* Version of this interface; raised whenever an entry point's signature or contract
+ * changes (2: moe_decode_gate_up takes the shared expert's rows; add + RMSNorm entry
+ * points; 3: no reserved zero head in the workspaces). */
+#define MOE_ABI_VERSION 3
 int moe_abi_version(void);
 const char* moe_last_error(void);
 
@@ -122,7 +120,7 @@ int moe_combine(const void* y, const void* w, int T, int H, int k, const void* y
                 const void* seg, long long ld_seg, const void* residual, void* out, int mode,
                 void* stream);
 
-/* Decode stages (T <= 4 tokens; H a multiple of 512 up to 4096, I and IS 512 or 1024,
+/* Decode stages (T <= 4 tokens; H 512, 1024, 2048 or 4096, I and IS 512 or 1024,
  * E <= 512, T*k <= 64): the three launches of engine/fast/fused.py's FusedDecode._moe
  * (fused.py:887-932). moe_decode_fits says whether a shape fits this path; the fused
  * entry points below take it on their own for such shapes with bf16 experts, and with

@@ -15,7 +15,7 @@ import torch  # noqa: F401  (loads the HIP runtime the library links against)
 
 LIB_PATH = Path(os.environ.get("MOE_MI355X_LIB", Path(__file__).resolve().parent / "libmoe_mi355x.so"))
 
-ABI_VERSION = 2  # MOE_ABI_VERSION of include/moe_mi355x.h that SIGNATURES describes
+ABI_VERSION = 3  # MOE_ABI_VERSION of include/moe_mi355x.h that SIGNATURES describes
 MOE_OK = 0
 MOE_EINVAL = 1
 MOE_EHIP = 2
@@ -125,22 +125,20 @@ def stream_of(t) -> int:
     return torch.cuda.current_stream(t.device).cuda_stream
 
 
-SYNC_BYTES = 4096  # the workspace head the fused kernels use as arrival counters
-
 _WORKSPACES: dict = {}
 
 
 def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     """A workspace of at least ``nbytes`` for calls on ``device``'s current stream.
 
-    One workspace is kept per (device, stream) and reused: its first ``SYNC_BYTES`` must be
-    zero before a call and every call leaves them zero (zeroed once at allocation, by a
-    fill kernel). Calls on one stream run in order, so they never share it concurrently."""
+    One workspace is kept per (device, stream) and reused (it is scratch: no call needs its
+    contents cleared). Calls on one stream run in order, so they never share it
+    concurrently."""
     idx = device.index if device.index is not None else torch.cuda.current_device()
     key = (idx, torch.cuda.current_stream(device).cuda_stream)
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
-        size = max(nbytes, SYNC_BYTES, 0 if ws is None else 2 * ws.numel())
-        ws = torch.zeros(size, dtype=torch.uint8, device=device)
+        size = max(nbytes, 256, 0 if ws is None else 2 * ws.numel())
+        ws = torch.empty(size, dtype=torch.uint8, device=device)
         _WORKSPACES[key] = ws
     return ws

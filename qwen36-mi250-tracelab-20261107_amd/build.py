@@ -59,9 +59,7 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
     with ThreadPoolExecutor(max_workers=jobs) as pool:
         objs = list(pool.map(_compile, sources))
     tmp = LIB.with_suffix(".so.tmp")
-    # hipBLASLt: the plain router GEMM of prefill-sized batches (router_blaslt.hip)
-    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs),
-           "-L/opt/rocm/lib", "-lhipblaslt", "-Wl,-rpath,/opt/rocm/lib", "-o", str(tmp)]
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr}")

@@ -540,7 +540,10 @@ __global__ __launch_bounds__(1024) void k_dec_down1(DecodeArgs a) {
 bool decode_fits(const DecodeArgs& a) {
   const int P = a.T * a.k;
   if (a.T < 1 || a.T > kDecMaxTokens || P > 64 || a.k < 1) return false;
-  if (a.H % 512 || a.H > 4096 || a.I % 512 || a.I > 1024 || a.I < 512) return false;
+  // hidden sizes of the instantiated kernels: 512 times 1, 2, 4 or 8
+  const int hc = a.H / 512;
+  if (a.H % 512 || (hc != 1 && hc != 2 && hc != 4 && hc != 8)) return false;
+  if (a.I % 512 || a.I > 1024 || a.I < 512) return false;
   if (a.logits && (a.E > 512 || a.E < 1)) return false;
   if (a.sh_down && (a.IS % 512 || a.IS > 1024 || a.IS < 512)) return false;
   return true;

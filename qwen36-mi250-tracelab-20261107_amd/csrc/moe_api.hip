@@ -25,8 +25,9 @@ hipError_t launch_route_sort(const uint16_t* logits, long long ld, const int* id
                              hipStream_t s);
 size_t sort_scratch_bytes(int P, int E);
 bool sort_uses_small(int P, int E);
-hipError_t launch_router_blaslt(const void* x, int T, int H, const void* w_pack, int n_pack,
-                                void* logits, hipStream_t st);
+bool router_gemm_fits(int H, int n_pack);
+hipError_t launch_router_gemm(const void* x, int T, int H, const void* w_pack, int n_pack,
+                              void* logits, hipStream_t st);
 hipError_t launch_combine(const uint16_t* y, const uint16_t* w, int k, const uint16_t* ysh,
                           const uint16_t* seg, long long ld_seg, const uint16_t* res, uint16_t* out,
                           int T, int H, int round_w, hipStream_t s);
@@ -124,10 +125,6 @@ bool decode_shared_in_gate_up() {
 
 size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
 
-// The first kSyncBytes of every workspace are reserved for cross-workgroup counters: zero
-// before the first call, and every call leaves them zero (no current kernel uses them).
-constexpr size_t kSyncBytes = 4096;
-
 // Sequential carve of a caller-provided workspace.
 struct Carver {
   char* base;
@@ -197,16 +194,19 @@ GemmOperand down_operand(const void* down, const float* scale, int H, int I, con
   return o;
 }
 
-// One launch for the routed experts and the shared expert, or two when their weight types
-// differ (fp8 experts, bf16 shared expert): the shared expert's tiles then come from the
-// token count alone (rows P .. P + T), not from the table.
 // A second stream per device for work that can run beside the caller's stream (forked and
 // joined with events, so it is ordered with the caller's work and is captured into the
 // caller's HIP graph as a parallel branch). Created on first use outside graph capture;
 // while none exists the work runs on the caller's stream. Default priority.
+// One stream per device, not one per caller stream: HIP maps streams onto its few hardware
+// queues round-robin, and with more streams the side branch can land on the caller's queue
+// and lose the overlap (measured at C4: 640 against 600 µs per layer). Calls from several
+// threads or caller streams are kept apart by the device's lock, held from fork to join
+// (see Fork).
 struct AuxStream {
   hipStream_t s = nullptr;
   hipEvent_t fork = nullptr, join = nullptr;
+  std::recursive_mutex mu;
 };
 AuxStream* aux_stream(hipStream_t caller) {
   static std::mutex mu;
@@ -225,12 +225,52 @@ AuxStream* aux_stream(hipStream_t caller) {
   }
   if (hipEventCreateWithFlags(&a.fork, hipEventDisableTiming) != hipSuccess ||
       hipEventCreateWithFlags(&a.join, hipEventDisableTiming) != hipSuccess) {
+    if (a.fork) hipEventDestroy(a.fork);
     hipStreamDestroy(a.s);
     a.s = nullptr;
     return nullptr;
   }
   return &a;
 }
+
+// One fork of the caller's stream onto the device's auxiliary stream. It holds the
+// auxiliary stream's lock for its lifetime, so the record / wait / launch / record / wait
+// sequence of one call never interleaves with another call's (another thread, another
+// caller stream) and a fork event is never re-recorded before its wait is queued. The join
+// runs on every path out of the scope that forked, errors included, so the caller's stream
+// (and a graph being captured on it) never returns with a branch left open.
+class Fork {
+ public:
+  Fork(AuxStream* aux, hipStream_t s) : aux_(aux), s_(s) {
+    if (aux_) lock_ = std::unique_lock<std::recursive_mutex>(aux_->mu);
+  }
+  Fork(const Fork&) = delete;
+  Fork& operator=(const Fork&) = delete;
+  ~Fork() { (void)join(); }
+  // Work queued on aux() after begin() waits for the caller's stream up to here.
+  hipError_t begin() {
+    if (!aux_) return hipSuccess;
+    hipError_t e = hipEventRecord(aux_->fork, s_);
+    if (e == hipSuccess) e = hipStreamWaitEvent(aux_->s, aux_->fork, 0);
+    open_ = e == hipSuccess;
+    return e;
+  }
+  // The caller's stream waits for the work queued on aux().
+  hipError_t join() {
+    if (!open_) return hipSuccess;
+    open_ = false;
+    hipError_t e = hipEventRecord(aux_->join, aux_->s);
+    if (e == hipSuccess) e = hipStreamWaitEvent(s_, aux_->join, 0);
+    return e;
+  }
+  hipStream_t aux() const { return aux_ ? aux_->s : s_; }
+
+ private:
+  AuxStream* aux_;
+  hipStream_t s_;
+  std::unique_lock<std::recursive_mutex> lock_;
+  bool open_ = false;
+};
 
 // Prefill tiles: the routed tiles fill whole rounds of one workgroup per CU (~256 experts x
 // 4 or 8 row blocks), and the shared expert's tiles would add a last, mostly idle round; run
@@ -242,23 +282,23 @@ hipError_t launch_prefill_split(int mode, const GemmArgs& a, int MT, hipStream_t
   GemmArgs v = a;  // no table: the prefill kernel reads tile i as shared rows [bm i, bm i + bm)
   v.op[0].N = 0;
   v.table = nullptr;
-  hipError_t e = hipEventRecord(aux->fork, s);
-  if (e == hipSuccess) e = hipStreamWaitEvent(aux->s, aux->fork, 0);
+  Fork fork(aux, s);
+  hipError_t e = fork.begin();
   if (e != hipSuccess) return e;
-  e = launch_prefill_gemm(mode, v, (a.T + prefill_tile_rows() - 1) / prefill_tile_rows(), aux->s);
+  e = launch_prefill_gemm(mode, v, (a.T + prefill_tile_rows() - 1) / prefill_tile_rows(),
+                          fork.aux());
   if (e != hipSuccess) return e;
   GemmArgs r = a;
   r.op[1].N = 0;
   e = launch_prefill_gemm(mode, r, MT, s);
   if (e != hipSuccess) return e;
-  e = hipEventRecord(aux->join, aux->s);
-  if (e == hipSuccess) e = hipStreamWaitEvent(s, aux->join, 0);
-  return e;
+  return fork.join();
 }
 
-// A launch whose routed experts are fp8 and shared expert bf16 runs as one launch whose
-// bf16 tiles take the kernel's bf16 body (mixed_enabled), or with MOE_MIXED=0 as two
-// launches, the shared one on the auxiliary stream so that the two overlap.
+// One launch for the routed experts and the shared expert, or two when their weight types
+// differ (fp8 experts, bf16 shared expert) and MOE_MIXED=0: then the shared expert's tiles
+// come from the token count alone (rows P .. P + T), on the auxiliary stream so that the two
+// launches overlap. By default (mixed_enabled) an fp8 launch takes the bf16 tiles itself.
 hipError_t launch_split(int mode, int role, int bm, const GemmArgs& a, int MT, hipStream_t s) {
   if (a.op[0].N <= 0 || a.op[1].N <= 0 || a.op[0].fp8 == a.op[1].fp8 || mixed_enabled())
     return launch_expert_gemm(mode, role, bm, a, MT, s);
@@ -266,23 +306,16 @@ hipError_t launch_split(int mode, int role, int bm, const GemmArgs& a, int MT, h
   v.op[0] = v.op[1];
   v.op[0].N = 0;
   v.table = nullptr;
-  AuxStream* aux = aux_stream(s);
-  hipStream_t vs = s;
-  if (aux) {
-    hipError_t e = hipEventRecord(aux->fork, s);
-    if (e == hipSuccess) e = hipStreamWaitEvent(aux->s, aux->fork, 0);
-    if (e != hipSuccess) return e;
-    vs = aux->s;
-  }
-  hipError_t err = launch_expert_gemm(mode, role, bm, v, (a.T + bm - 1) / bm, vs);
+  Fork fork(aux_stream(s), s);
+  hipError_t err = fork.begin();
+  if (err != hipSuccess) return err;
+  err = launch_expert_gemm(mode, role, bm, v, (a.T + bm - 1) / bm, fork.aux());
   if (err != hipSuccess) return err;
   GemmArgs r = a;
   r.op[1].N = 0;
   err = launch_expert_gemm(mode, role, bm, r, MT, s);
-  if (err != hipSuccess || !aux) return err;
-  err = hipEventRecord(aux->join, aux->s);
-  if (err == hipSuccess) err = hipStreamWaitEvent(s, aux->join, 0);
-  return err;
+  if (err != hipSuccess) return err;
+  return fork.join();
 }
 
 // Which projections a grouped launch runs: both weight families (split as above when
@@ -400,13 +433,12 @@ int moe_max_tiles(int T, int k, int E, int bm, int has_shared) {
 }  // extern "C"
 
 namespace {
-// From this many tokens the router uses hipBLASLt (measured: 8.9 µs against 13.4 at 512
-// tokens, 15 against 38 at 4096; below 256 the expert GEMM's small tiles are as fast).
-constexpr int kRouterBlasltMinTokens = 256;
-
-// Router GEMM (PLAIN, identity tiles over the tokens).
+// Router GEMM: k_router_gemm (router_gemm.hip), whose per-logit summation order is the same
+// at every batch size; shapes it does not take (hidden not a multiple of 128) use the expert
+// GEMM's 16-token identity tiles with K split over 8 waves, also one order for every T.
 hipError_t launch_router(const void* x, int T, int H, const void* w_pack, int n_pack,
                          void* logits, hipStream_t st) {
+  if (router_gemm_fits(H, n_pack)) return launch_router_gemm(x, T, H, w_pack, n_pack, logits, st);
   GemmArgs a{};
   GemmOperand& v = a.op[1];
   v.w = w_pack;
@@ -423,26 +455,7 @@ hipError_t launch_router(const void* x, int T, int H, const void* w_pack, int n_
   a.P = 0;
   a.E = 0;
   a.T = T;
-  // Token rows per tile: 16-token tiles with K split over 8 waves for every batch below the
-  // hipBLASLt threshold (measured per call: 6.6 / 6.6 / 7.1 / 10.6 µs at 64 / 100 / 200 /
-  // 255 tokens against 24.9 µs with 32-token tiles). One configuration also keeps each
-  // logit's fp32 summation order independent of the batch size, so a token's routing does
-  // not depend on the tokens batched with it. Without a hipBLASLt plan larger batches use
-  // 32-token tiles up to 1024 tokens and 64 above.
-  int bm = T < kRouterBlasltMinTokens ? 16 : (T <= 1024 ? 32 : 64);
-  const char* env_bm = getenv("MOE_ROUTER_BM");
-  if (env_bm) bm = atoi(env_bm);
-  // prefill-sized batches: the plain GEMM through hipBLASLt when it has a plan
-  if (T >= kRouterBlasltMinTokens && !env_bm) {
-    hipError_t err = launch_router_blaslt(x, T, H, w_pack, n_pack, logits, st);
-    if (err != hipErrorInvalidValue) return err;
-  }
-  if (bm == prefill_tile_rows()) {
-    hipError_t err = launch_prefill_gemm(kModePlain, a, (T + bm - 1) / bm, st);
-    if (err != hipErrorInvalidValue) return err;
-    bm = 16;
-  }
-  return launch_expert_gemm(kModePlain, kRoleRouter, bm, a, (T + bm - 1) / bm, st);
+  return launch_expert_gemm(kModePlain, kRoleRouter, 16, a, (T + 15) / 16, st);
 }
 }  // namespace
 
@@ -556,7 +569,8 @@ int moe_decode_router(const void* x, int T, int H, const void* w_pack, int n_pac
                       void* stream) {
   CHECK_ARG(x && w_pack && logits, "null pointer");
   CHECK_ARG(!sh_gate || (sh_up && act_sh), "shared gate without shared up / act_sh");
-  CHECK_ARG(T >= 1 && T <= kDecMaxTokens && H % 512 == 0 && H <= 4096 && n_pack >= 1,
+  CHECK_ARG(T >= 1 && T <= kDecMaxTokens && n_pack >= 1 &&
+                (H == 512 || H == 1024 || H == 2048 || H == 4096),
             "decode router shape (T=%d H=%d n_pack=%d) not supported", T, H, n_pack);
   CHECK_ARG(!sh_gate || (IS >= 1), "bad shared intermediate %d", IS);
   DecodeArgs d{};
@@ -641,7 +655,6 @@ int moe_decode_down(const void* act, int T, int H, int E, int k, int I, const in
 
 namespace {
 struct ExpertsWs {
-  int* sync;
   int *idx32, *counts, *offsets, *order, *table, *scratch;
   uint16_t *act, *y;
   size_t bytes;
@@ -653,7 +666,6 @@ ExpertsWs carve_experts(void* base, int T, int H, int E, int k, int I, bool fp8)
   const int P = T * k;
   w.bm = tile_rows_for(T, fp8, H, I, I);
   w.MT = max_tiles_of(T, k, E, w.bm, 0);
-  w.sync = c.take<int>(kSyncBytes / sizeof(int));
   w.idx32 = c.take<int>(P);
   w.counts = c.take<int>(E);
   w.offsets = c.take<int>(E);
@@ -728,7 +740,6 @@ int moe_experts_forward(const void* x, int T, int H, int E, int k, int I,
 
 namespace {
 struct BlockWs {
-  int* sync;
   uint16_t* logits;
   long long* idx64;
   int* idx32;
@@ -745,7 +756,6 @@ BlockWs carve_block(void* base, int T, int H, int E, int k, int I, int IS, int n
   const int P = T * k;
   w.bm = tile_rows_for(T, fp8, H, I, IS);
   w.MT = max_tiles_of(T, k, E, w.bm, 1);
-  w.sync = c.take<int>(kSyncBytes / sizeof(int));
   w.logits = c.take<uint16_t>((size_t)T * n_pack);
   w.idx64 = c.take<long long>(P);
   w.idx32 = c.take<int>(P);
@@ -851,14 +861,14 @@ int block_forward(const void* x, int T, int H, int E, int k, int I, int IS, cons
   AuxStream* aux = block_side_enabled(T, wdtype == MOE_WEIGHTS_FP8_E4M3, w.bm) ? aux_stream(s)
                                                                                : nullptr;
   const int part = aux ? kRoutedOnly : kBoth;
+  Fork fork(aux, s);  // joined before the combine, or on any early return
   if (aux) {
-    HIP_TRY(hipEventRecord(aux->fork, s), "fork");
-    HIP_TRY(hipStreamWaitEvent(aux->s, aux->fork, 0), "fork");
+    HIP_TRY(fork.begin(), "fork");
     rc = run_gate_up(x, T, H, E, k, I, gate_up, gu_scale, wdtype, sh_gate, sh_up, IS, w.order,
-                     w.table, w.MT, w.bm, w.act, w.act_sh, aux->s, kSharedOnly);
+                     w.table, w.MT, w.bm, w.act, w.act_sh, fork.aux(), kSharedOnly);
     if (rc) return rc;
     rc = run_down(w.act, T, H, E, k, I, down, dn_scale, wdtype, sh_down, IS, w.act_sh, w.order,
-                  w.table, w.MT, w.bm, w.y, w.y_sh, aux->s, kSharedOnly);
+                  w.table, w.MT, w.bm, w.y, w.y_sh, fork.aux(), kSharedOnly);
     if (rc) return rc;
   }
   rc = moe_router_logits(x, T, H, w_pack, n_pack, lg, stream);
@@ -873,10 +883,7 @@ int block_forward(const void* x, int T, int H, int E, int k, int I, int IS, cons
   rc = run_down(w.act, T, H, E, k, I, down, dn_scale, wdtype, sh_down, IS, w.act_sh, w.order,
                 w.table, w.MT, w.bm, w.y, w.y_sh, s, part);
   if (rc) return rc;
-  if (aux) {
-    HIP_TRY(hipEventRecord(aux->join, aux->s), "join");
-    HIP_TRY(hipStreamWaitEvent(s, aux->join, 0), "join");
-  }
+  HIP_TRY(fork.join(), "join");
   return hip_check(launch_combine(w.y, wt, k, w.y_sh, lg + E, n_pack,
                                   static_cast<const uint16_t*>(residual),
                                   static_cast<uint16_t*>(out), T, H, mode == MOE_ROUND_PRODUCT, s),

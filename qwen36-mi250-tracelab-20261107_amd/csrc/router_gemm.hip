@@ -1,0 +1,211 @@
+// Router logits of tiled batches (more than the decode path's few tokens) on gfx950
+// (subsystem a1): logits[t, n] = bf16(x_t . w_pack[n]) with fp32 accumulation, the router
+// F.linear of modeling_qwen3_5_moe.py:768-769 / engine/fast/model.py:1159 and the merged
+// projection of engine/fast/prefill_kernels.py:91 (`project`, used at :693).
+//
+// Batch invariance. Every logit is summed in ONE fixed order whatever the batch size or
+// the tile configuration: K (the hidden size) is split into four quarters, wave w of a
+// workgroup sums quarter w with v_mfma_f32_16x16x32_bf16 k-steps of 32 in ascending order,
+// and the four partial sums are added as ((s0 + s1) + s2) + s3. The tile shape (how many
+// 16-token and 16-row blocks a wave holds) only changes which outputs a workgroup makes, not
+// how any one of them is summed, so the configuration can follow the batch size and a
+// token's logits (hence its routing) never depend on the tokens batched with it.
+//
+// Work decomposition. No operand is shared between the waves of a workgroup (each wave
+// needs its own K quarter of both), so both operands go straight from global memory into
+// registers in the MFMA operand layout (lane l: row l % 16, k = 8 (l / 16) .. + 8; 64
+// contiguous bytes of each of 16 rows per load instruction), R k-steps in flight per wave.
+// LDS is used only for the final reduction. Workgroups of one token tile get ids 8 apart so
+// they run on one XCD and share the tile's token rows in its L2 (the router rows, 1.25 MiB,
+// stay in every XCD's L2).
+#include <stdio.h>
+#include <stdlib.h>
+
+#include "moe_common.h"
+
+namespace moe {
+
+namespace {
+
+constexpr int kRouterSplit = 4;  // K quarters = waves per workgroup (fixes the sum order)
+constexpr int kXcdsR = 8;
+
+struct RouterArgs {
+  const uint16_t* x;  // [T, H]
+  const uint16_t* w;  // [n_pack, H]
+  uint16_t* out;      // [T, n_pack]
+  int T, H, n_pack;
+  int ntiles, nrg;    // token tiles, row groups
+  int xcd_map;        // workgroups of one token tile 8 ids apart (at least 8 tiles)
+};
+
+// TB 16-token blocks x RB 16-row blocks per wave; R k-steps of loads in flight.
+template <int TB, int RB, int R>
+__global__ __launch_bounds__(64 * kRouterSplit) void k_router_gemm(RouterArgs a) {
+  __shared__ f32x4_t red[kRouterSplit - 1][TB * RB][kWave];
+  int tile, rg;
+  if (a.xcd_map) {
+    const int xcd = blockIdx.x & (kXcdsR - 1);
+    const int j = blockIdx.x / kXcdsR;
+    tile = (j / a.nrg) * kXcdsR + xcd;
+    rg = j - (j / a.nrg) * a.nrg;
+    if (tile >= a.ntiles) return;
+  } else {
+    tile = blockIdx.x / a.nrg;
+    rg = blockIdx.x - tile * a.nrg;
+  }
+
+  const int lane = threadIdx.x & 63;
+  const int wk = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lr = lane & 15;
+  const int q = lane >> 4;
+  const int Kq = a.H / kRouterSplit;
+  const int kbeg = wk * Kq;
+  const int nst = Kq / 32;
+  const int t0 = tile * 16 * TB;
+  const int n0 = rg * 16 * RB;
+  // blocks that hold real rows / tokens (wave-uniform: n_pack is a multiple of 16)
+  const int nrb = __builtin_amdgcn_readfirstlane(min(RB, (a.n_pack - n0) / 16));
+  const int ntb = __builtin_amdgcn_readfirstlane(min(TB, (a.T - t0 + 15) / 16));
+
+  const uint16_t* wa[RB];
+  const uint16_t* xb[TB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
+    wa[rb] = a.w + (long long)min(n0 + rb * 16 + lr, a.n_pack - 1) * a.H + kbeg + q * 8;
+#pragma unroll
+  for (int tb = 0; tb < TB; ++tb)
+    xb[tb] = a.x + (long long)min(t0 + tb * 16 + lr, a.T - 1) * a.H + kbeg + q * 8;
+
+  uint4 ra[R][RB], rx[R][TB];
+  auto issue = [&](int slot, int s) {
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+      if (rb < nrb) ra[slot][rb] = ld16(wa[rb] + s * 32);
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb)
+      if (tb < ntb) rx[slot][tb] = ld16(xb[tb] + s * 32);
+  };
+#pragma unroll
+  for (int s = 0; s < R; ++s)
+    if (s < nst) issue(s, s);
+
+  f32x4_t acc[TB][RB];
+#pragma unroll
+  for (int tb = 0; tb < TB; ++tb)
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) acc[tb][rb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  for (int s0 = 0; s0 < nst; s0 += R) {
+#pragma unroll
+    for (int c = 0; c < R; ++c) {
+      const int s = s0 + c;
+      if (s >= nst) break;
+#pragma unroll
+      for (int tb = 0; tb < TB; ++tb)
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+          if (tb < ntb && rb < nrb) acc[tb][rb] = mfma16x16x32(ra[c][rb], rx[c][tb], acc[tb][rb]);
+      if (s + R < nst) issue(c, s + R);
+    }
+  }
+
+  // ((s0 + s1) + s2) + s3 in wave order
+  if (wk > 0) {
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb)
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) red[wk - 1][tb * RB + rb][lane] = acc[tb][rb];
+  }
+  __syncthreads();
+  if (wk > 0) return;
+#pragma unroll
+  for (int v = 0; v < kRouterSplit - 1; ++v)
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb)
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) acc[tb][rb] += red[v][tb * RB + rb][lane];
+
+  // lane (q, j = lr) holds rows 4q .. 4q + 3 of token column j of each block
+#pragma unroll
+  for (int tb = 0; tb < TB; ++tb) {
+    const int t = t0 + tb * 16 + lr;
+    if (tb >= ntb || t >= a.T) continue;
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      if (rb >= nrb) break;
+      const int n = n0 + rb * 16 + 4 * q;
+      const f32x4_t v = acc[tb][rb];
+      *reinterpret_cast<uint2*>(a.out + (long long)t * a.n_pack + n) =
+          make_uint2(pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3]));
+    }
+  }
+}
+
+struct RCfg {
+  int tb, rb, r;
+};
+
+// Tile configuration by batch size (it does not change any logit's bits). Measured per
+// call at H=2048, n_pack=320 (8 launches graph-replayed): T <= 128 (1,1,4) 6.1-6.2 µs;
+// 256 (2,1,8) 9.3; 512 (2,2,4) 11.4; 1024 (4,2,4) 15.9; 2048 (4,4,4) 21.1; 4096 (4,4,2)
+// 39.7. MOE_ROUTER_CFG "tb,rb,r" overrides it (tuning knob).
+RCfg router_cfg(int T) {
+  const char* env = getenv("MOE_ROUTER_CFG");
+  RCfg c{};
+  if (env && sscanf(env, "%d,%d,%d", &c.tb, &c.rb, &c.r) == 3) return c;
+  if (T <= 128) return {1, 1, 4};
+  if (T <= 384) return {2, 1, 8};
+  if (T <= 768) return {2, 2, 4};
+  if (T <= 1536) return {4, 2, 4};
+  if (T <= 3072) return {4, 4, 4};
+  return {4, 4, 2};
+}
+
+}  // namespace
+
+bool router_gemm_fits(int H, int n_pack) { return H % (32 * kRouterSplit) == 0 && n_pack % 16 == 0; }
+
+hipError_t launch_router_gemm(const void* x, int T, int H, const void* w_pack, int n_pack,
+                              void* logits, hipStream_t st) {
+  if (!router_gemm_fits(H, n_pack)) return hipErrorInvalidValue;
+  if (T <= 0) return hipSuccess;
+  const RCfg c = router_cfg(T);
+  RouterArgs a{};
+  a.x = static_cast<const uint16_t*>(x);
+  a.w = static_cast<const uint16_t*>(w_pack);
+  a.out = static_cast<uint16_t*>(logits);
+  a.T = T;
+  a.H = H;
+  a.n_pack = n_pack;
+  a.ntiles = (T + 16 * c.tb - 1) / (16 * c.tb);
+  a.nrg = (n_pack + 16 * c.rb - 1) / (16 * c.rb);
+  a.xcd_map = a.ntiles >= kXcdsR;
+  const long long grid = a.xcd_map
+                             ? (long long)((a.ntiles + kXcdsR - 1) / kXcdsR) * kXcdsR * a.nrg
+                             : (long long)a.ntiles * a.nrg;
+  if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
+  const dim3 block(64 * kRouterSplit);
+#define RL(TB, RB, RR)                                                                   \
+  if (c.tb == TB && c.rb == RB && c.r == RR) {                                           \
+    hipLaunchKernelGGL((k_router_gemm<TB, RB, RR>), dim3((unsigned)grid), block, 0, st, a); \
+    return hipGetLastError();                                                            \
+  }
+  RL(1, 1, 8)
+  RL(1, 1, 4)
+  RL(1, 1, 16)
+  RL(1, 2, 8)
+  RL(2, 1, 8)
+  RL(2, 2, 8)
+  RL(2, 2, 4)
+  RL(4, 1, 8)
+  RL(1, 4, 8)
+  RL(4, 2, 4)
+  RL(2, 4, 4)
+  RL(4, 4, 4)
+  RL(4, 4, 2)
+#undef RL
+  return hipErrorInvalidValue;
+}
+
+}  // namespace moe

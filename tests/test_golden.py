@@ -68,4 +68,10 @@ def test_gpu_block_on_golden(pkg, dev, name):
     assert torch.equal(idx.cpu(), _tie_rule(t["top_k_index"], t["logits"]))
     assert max_abs(out.cpu(), t["out"]) <= 2e-2
     f32 = orc.block_fp32(t["x"], w, t["top_k_index"], logits=t["logits"])
-    assert max_abs(out.cpu(), f32) <= 2e-2 and mean_rel(out.cpu(), f32) <= 1e-2
+    print(f"golden {name}: vs fixture max {max_abs(out.cpu(), t['out']):.3g}; vs fp32 max "
+          f"{max_abs(out.cpu(), f32):.3g} mean-rel {mean_rel(out.cpu(), f32):.3g}; fixture vs fp32 "
+          f"mean-rel {mean_rel(t['out'], f32):.3g}", flush=True)
+    # measured: bit-equal to the fixture (the Transformers block's own output), whose
+    # mean-rel to fp32 is 4.2e-3 / 4.9e-3
+    assert max_abs(out.cpu(), f32) <= 2e-3
+    assert mean_rel(out.cpu(), f32) <= max(5e-3, 1.1 * mean_rel(t["out"], f32))

@@ -237,3 +237,29 @@ def test_decode_gate_up_hard_routing_rows(pkg, dev, E, k):
         d = (wts.float().cpu() - ref_w.float()).abs()
         assert (d <= ref_w.float().abs() * 2.0 ** -7 + 1e-30).all(), f"row {r}"
         assert torch.equal(act, act2), f"row {r}"
+
+
+@pytest.mark.parametrize("T", [1, 3])
+def test_hidden_1536_takes_tiled_path(pkg, dev, T):
+    """H = 1536 (a multiple of 512 the decode kernels are not built for) at decode sizes:
+    the block takes the tiled path and matches the oracle."""
+    import __graft_entry__
+
+    H, E, K, I = 1536, 32, 4, 512
+    w = orc.make_weights(H, E, I, I, seed=15)
+    g = torch.Generator().manual_seed(T)
+    x = torch.randn(T, H, generator=g).to(BF16)
+    mlp = __graft_entry__._mlp_from_weights(w, dev)
+    out, idx, wts, logits = pkg.block.moe(x.to(dev), mlp, K, decode=True, return_routing=True)
+    torch.cuda.synchronize()
+    lg = logits.cpu()[:, :E]
+    ref_w, ref_i = orc.route(lg, K)
+    assert torch.equal(idx.cpu(), ref_i)
+    f32 = orc.block_fp32(x, w, ref_i, logits=lg)
+    wc, ic = orc.compact_experts(w, ref_i)
+    ref = orc.block_bf16_routed(x, wc, ic, wts.cpu(), logits.cpu()[:, E:E + 1], decode=True)
+    ours, theirs = mean_rel(out, f32), mean_rel(ref, f32)
+    print(f"H=1536 T={T}: max {max_abs(out, f32):.3g} mean-rel {ours:.3g} "
+          f"(reference path {theirs:.3g})", flush=True)
+    assert max_abs(out, f32) <= 2e-2 and max_abs(out, ref) <= 2e-2
+    assert ours <= max(5e-3, 1.1 * theirs)

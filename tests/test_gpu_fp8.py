@@ -64,7 +64,10 @@ def test_fp8_experts_match_dequantised_oracle(pkg, dev, n):
             gu = deq["gate_up"][e] @ x[t].float()
             a = torch.nn.functional.silu(gu[:I]) * gu[I:]
             ref[t] += tw[t, j].float() * (deq["down"][e] @ a)
-    assert max_abs(out, ref) <= 2e-2 and mean_rel(out, ref) <= 1e-2
+    print(f"fp8 experts n={n}: vs dequantised fp32 max {max_abs(out, ref):.3g} "
+          f"mean-rel {mean_rel(out, ref):.3g}", flush=True)
+    # measured max-abs 1.2e-4, mean-rel 4.0e-3 - 4.4e-3 (bf16 rounding of the projections)
+    assert max_abs(out, ref) <= 1e-3 and mean_rel(out, ref) <= 5e-3
 
 
 @pytest.mark.parametrize("T", [1, 32])

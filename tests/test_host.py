@@ -32,7 +32,7 @@ def test_library_exports_every_declared_symbol(pkg):
         assert hasattr(lib, name), name
         assert name in pkg._lib.SIGNATURES, f"{name} has no ctypes signature"
     assert set(pkg._lib.SIGNATURES) == set(_declared_symbols())
-    assert lib.moe_abi_version() == pkg._lib.ABI_VERSION == 2
+    assert lib.moe_abi_version() == pkg._lib.ABI_VERSION == 3
 
 
 @pytest.mark.parametrize("T,k,E,bm,sh", [(1, 8, 256, 64, 1), (64, 8, 256, 64, 1),
@@ -128,3 +128,11 @@ def test_add_rms_argument_checks_before_any_launch(pkg):
     # total overlapping the input
     assert lib.moe_block_forward_add_rms(X, Hh, W, 1e-6, *args, X, OUT, OUT + (1 << 16), None,
                                          None, None, P, ws, None) == EINVAL
+
+
+@pytest.mark.parametrize("H,fits", [(512, 1), (1024, 1), (2048, 1), (4096, 1), (1536, 0),
+                                    (2560, 0), (3072, 0), (3584, 0), (8192, 0)])
+def test_decode_fits_only_instantiated_hidden_sizes(pkg, H, fits):
+    """The decode kernels are instantiated for H = 512 x {1, 2, 4, 8}; other multiples of
+    512 go to the tiled path instead of failing at launch."""
+    assert pkg._lib.load().moe_decode_fits(1, H, 256, 8, 512, 512) == fits
