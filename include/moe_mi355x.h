@@ -183,6 +183,24 @@ int moe_block_forward(const void* x, int T, int H, int E, int k, int I, int IS,
                       void* out, long long* top_k_index, void* top_k_weights, void* logits,
                       void* workspace, size_t workspace_bytes, void* stream);
 
+/* Whole block without a caller workspace (no counterpart in the reference): for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). Same arguments and results as moe_block_forward, minus
+ * workspace / workspace_bytes: the workspace is a static device array of
+ * MOE_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends, whose address is looked
+ * up on the first call on each device. Calls whose moe_block_workspace_bytes(...) exceeds
+ * it fail with MOE_EINVAL (at the full Qwen3.6 layer shape: up to ~350 tokens). No call
+ * allocates or frees anything. Every call on one GPU uses that GPU's one array: calls that
+ * overlap on one GPU (two streams, two threads) race and must be serialised by the caller. */
+#define MOE_NOALLOC_SCRATCH_BYTES (16u << 20)
+int moe_block_forward_noalloc(const void* x, int T, int H, int E, int k, int I, int IS,
+                              const void* w_pack, int n_pack, const void* gate_up,
+                              const float* gu_scale, const void* down, const float* dn_scale,
+                              int wdtype, const void* sh_gate, const void* sh_up,
+                              const void* sh_down, const void* residual, int mode, void* out,
+                              long long* top_k_index, void* top_k_weights, void* logits,
+                              void* stream);
+
 /* Post-attention residual add + zero-centred RMSNorm: total = bf16(x + h) and
  * out = bf16(total * rsqrt(mean(total^2) + eps) * (1 + weight)), fp32 in between; h null:
  * no add (total is not written, the norm is of x). x, h, total, out [T, H] bf16 with

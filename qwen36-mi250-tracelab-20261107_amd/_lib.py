@@ -23,6 +23,7 @@ WEIGHTS_BF16 = 0
 WEIGHTS_FP8_E4M3 = 1
 ROUND_PRODUCT = 1
 EXACT_PRODUCT = 2
+NOALLOC_SCRATCH_BYTES = 16 << 20  # MOE_NOALLOC_SCRATCH_BYTES: moe_block_forward_noalloc's limit
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -62,6 +63,11 @@ SIGNATURES: dict[str, tuple] = {
         _I,
         [_P, _I, _I, _I, _I, _I, _I, _P, _I, _P, _P, _P, _P, _I, _P, _P, _P, _P, _I,
          _P, _P, _P, _P, _P, _SZ, _P],
+    ),
+    "moe_block_forward_noalloc": (
+        _I,
+        [_P, _I, _I, _I, _I, _I, _I, _P, _I, _P, _P, _P, _P, _I, _P, _P, _P, _P, _I,
+         _P, _P, _P, _P, _P],
     ),
     "moe_add_rmsnorm": (_I, [_P, _P, _P, _I, _I, _F, _P, _P, _P]),
     "moe_block_forward_add_rms": (

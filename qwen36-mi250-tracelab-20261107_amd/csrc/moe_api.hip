@@ -933,6 +933,71 @@ int moe_block_forward(const void* x, int T, int H, int E, int k, int I, int IS,
                        top_k_weights, logits, workspace, workspace_bytes, stream, nullptr);
 }
 
+}  // extern "C"
+
+// ------------------------------------------------------------- no-allocation variant
+
+namespace {
+
+// The no-allocation entry point's workspace: a file-scope device array, one copy per GPU,
+// held until the process ends. Host code never passes `scratch` itself to a kernel or a
+// copy (in host code the name is a host-side stand-in, not a device address): it uses the
+// address hipGetSymbolAddress gives for the current device, looked up once per device.
+constexpr size_t kNoAllocScratchBytes = MOE_NOALLOC_SCRATCH_BYTES;
+__device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+// The device address of `scratch` on the current device (looked up on the device's first
+// call), or null with the error in moe_last_error().
+void* scratch_ptr() {
+  static std::mutex mu;
+  static void* ptrs[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    fail(MOE_EHIP, "no-alloc block: no current HIP device");
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  if (!ptrs[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      fail(MOE_EHIP, "no-alloc block: hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+      return nullptr;
+    }
+    ptrs[dev] = p;
+  }
+  return ptrs[dev];
+}
+
+}  // namespace
+
+extern "C" {
+
+int moe_block_forward_noalloc(const void* x, int T, int H, int E, int k, int I, int IS,
+                              const void* w_pack, int n_pack, const void* gate_up,
+                              const float* gu_scale, const void* down, const float* dn_scale,
+                              int wdtype, const void* sh_gate, const void* sh_up,
+                              const void* sh_down, const void* residual, int mode, void* out,
+                              long long* top_k_index, void* top_k_weights, void* logits,
+                              void* stream) {
+  if (T < 0 || k < 1 || E < 1) return fail(MOE_EINVAL, "bad T/k/E (%d, %d, %d)", T, k, E);
+  const size_t need = moe_block_workspace_bytes(T, H, E, k, I, IS, n_pack);
+  CHECK_ARG(need <= kNoAllocScratchBytes,
+            "no-alloc block: this call needs %zu bytes of workspace, more than the %zu of the "
+            "static scratch (fewer tokens per call, or moe_block_forward with a workspace)",
+            need, kNoAllocScratchBytes);
+  if (T == 0)
+    return block_forward(x, T, H, E, k, I, IS, w_pack, n_pack, gate_up, gu_scale, down,
+                         dn_scale, wdtype, sh_gate, sh_up, sh_down, residual, mode, out,
+                         top_k_index, top_k_weights, logits, nullptr, 0, stream, nullptr);
+  void* ws = scratch_ptr();
+  if (!ws) return MOE_EHIP;
+  // nothing in a block workspace needs to start at zero: every kernel writes what it reads
+  return block_forward(x, T, H, E, k, I, IS, w_pack, n_pack, gate_up, gu_scale, down, dn_scale,
+                       wdtype, sh_gate, sh_up, sh_down, residual, mode, out, top_k_index,
+                       top_k_weights, logits, ws, kNoAllocScratchBytes, stream, nullptr);
+}
+
 int moe_add_rmsnorm(const void* x, const void* h, const void* weight, int T, int H, float eps,
                     void* total, void* out, void* stream) {
   const int rc = check_norm_args(x, h, weight, T, H, eps, total, out, nullptr);
