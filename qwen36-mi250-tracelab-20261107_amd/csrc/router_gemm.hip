@@ -11,13 +11,19 @@
 // how any one of them is summed, so the configuration can follow the batch size and a
 // token's logits (hence its routing) never depend on the tokens batched with it.
 //
-// Work decomposition. No operand is shared between the waves of a workgroup (each wave
-// needs its own K quarter of both), so both operands go straight from global memory into
-// registers in the MFMA operand layout (lane l: row l % 16, k = 8 (l / 16) .. + 8; 64
-// contiguous bytes of each of 16 rows per load instruction), R k-steps in flight per wave.
-// LDS is used only for the final reduction. Workgroups of one token tile get ids 8 apart so
-// they run on one XCD and share the tile's token rows in its L2 (the router rows, 1.25 MiB,
-// stay in every XCD's L2).
+// Two kernels give those bits:
+// * k_router_gemm (up to ~1k tokens): K split over the 4 waves of a workgroup. No operand is
+//   shared between its waves (each needs its own K quarter of both), so both go straight
+//   from global memory into registers in the MFMA operand layout (lane l: row l % 16,
+//   k = 8 (l / 16) .. + 8; 64 contiguous bytes of each of 16 rows per load instruction), R
+//   k-steps in flight per wave; LDS holds only the final reduction.
+// * k_router_tiles (prefill-sized batches): 64 tokens x 64 rows per workgroup, both operands
+//   staged through LDS and shared by 4 waves (2 x 2 blocks of 16 each); each wave runs the
+//   whole K, restarting its accumulator at every quarter and folding it into a running
+//   total, which reproduces ((s0 + s1) + s2) + s3 bit for bit with a quarter of the operand
+//   traffic of the split kernel.
+// Workgroups of one token tile get ids 8 apart so they run on one XCD and share the tile's
+// token rows in its L2 (the router rows, 1.25 MiB, stay in every XCD's L2).
 #include <stdio.h>
 #include <stdlib.h>
 
@@ -29,6 +35,7 @@ namespace {
 
 constexpr int kRouterSplit = 4;  // K quarters = waves per workgroup (fixes the sum order)
 constexpr int kXcdsR = 8;
+constexpr int kRouterTilesFrom = 768;  // tokens from which the LDS-tiled kernel runs
 
 struct RouterArgs {
   const uint16_t* x;  // [T, H]
@@ -142,14 +149,126 @@ __global__ __launch_bounds__(64 * kRouterSplit) void k_router_gemm(RouterArgs a)
   }
 }
 
+// ------------------------------------------------------------------ LDS-tiled form
+
+constexpr int kTT = 64;                 // tokens per tile
+constexpr int kTN = 64;                 // router rows per tile
+constexpr int kTRows = kTT + kTN;       // staged rows per chunk (tokens, then router rows)
+
+// KC: k per staged chunk (KC / 8 16-byte units of each row; one barrier per chunk).
+template <int KC>
+__global__ __launch_bounds__(256) void k_router_tiles(RouterArgs a) {
+  constexpr int kTK = KC;
+  constexpr int kTUnits = kTK / 8;
+  constexpr int kTStageU4 = kTRows * kTUnits;  // one stage in uint4
+  constexpr int kTLoads = kTStageU4 / 256;     // 16-byte loads per thread per chunk
+  __shared__ uint4 lds[2 * kTStageU4];
+  int tile, rg;
+  if (a.xcd_map) {
+    const int xcd = blockIdx.x & (kXcdsR - 1);
+    const int j = blockIdx.x / kXcdsR;
+    tile = (j / a.nrg) * kXcdsR + xcd;
+    rg = j - (j / a.nrg) * a.nrg;
+    if (tile >= a.ntiles) return;
+  } else {
+    tile = blockIdx.x / a.nrg;
+    rg = blockIdx.x - tile * a.nrg;
+  }
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wt = wave & 1, wn = wave >> 1;  // token half, row half of the tile
+  const int lr = lane & 15, kq = lane >> 4;
+  const int t0 = tile * kTT, n0 = rg * kTN;
+
+  // staging: thread tid moves 16-byte unit (tid + 256 i) of the chunk: row = u / kTUnits
+  // (tokens 0..63, then router rows), physical unit u % kTUnits holding logical unit
+  // (u % kTUnits) ^ (row % kTUnits)
+  const uint16_t* src[kTLoads];
+  int dst[kTLoads];
+#pragma unroll
+  for (int i = 0; i < kTLoads; ++i) {
+    const int u = tid + 256 * i;
+    const int row = u / kTUnits, pu = u % kTUnits;
+    const int lu = pu ^ (row & (kTUnits - 1));
+    src[i] = row < kTT ? a.x + (long long)min(t0 + row, a.T - 1) * a.H + lu * 8
+                       : a.w + (long long)min(n0 + row - kTT, a.n_pack - 1) * a.H + lu * 8;
+    dst[i] = u;
+  }
+  uint4 stage[kTLoads];
+  auto load = [&](int d) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < kTLoads; ++i) stage[i] = ld16(src[i] + d * kTK);
+  };
+  auto store = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < kTLoads; ++i) lds[buf * kTStageU4 + dst[i]] = stage[i];
+  };
+
+  f32x4_t acc[2][2], tot[2][2];  // [token block][row block]
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int r = 0; r < 2; ++r) acc[b][r] = tot[b][r] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  const int nd = a.H / kTK;                      // chunks
+  const int per_q = nd / kRouterSplit;           // chunks per K quarter
+  load(0);
+  store(0);
+  if (nd > 1) load(1);
+  for (int d = 0; d < nd; ++d) {
+    __syncthreads();  // chunk d staged; the other buffer free
+    if (d + 1 < nd) store((d + 1) & 1);
+    if (d + 2 < nd) load(d + 2);
+    const uint4* st = lds + (d & 1) * kTStageU4;
+#pragma unroll
+    for (int h = 0; h < kTK / 32; ++h) {
+      const int lu = (h * 4 + kq) ^ (lr & (kTUnits - 1));
+      uint4 fa[2], fb[2];
+#pragma unroll
+      for (int r = 0; r < 2; ++r) fa[r] = st[(kTT + wn * 32 + r * 16 + lr) * kTUnits + lu];
+#pragma unroll
+      for (int b = 0; b < 2; ++b) fb[b] = st[(wt * 32 + b * 16 + lr) * kTUnits + lu];
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int r = 0; r < 2; ++r) acc[b][r] = mfma16x16x32(fa[r], fb[b], acc[b][r]);
+    }
+    if ((d + 1) % per_q == 0) {  // end of a K quarter: total = ((s0 + s1) + s2) + s3
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+          tot[b][r] = d + 1 == per_q ? acc[b][r] : tot[b][r] + acc[b][r];
+          acc[b][r] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        }
+    }
+  }
+  // lane (q = kq, j = lr) holds rows 4q .. 4q + 3 of token column j of each block
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    const int t = t0 + wt * 32 + b * 16 + lr;
+    if (t >= a.T) continue;
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int n = n0 + wn * 32 + r * 16 + 4 * kq;
+      if (n >= a.n_pack) continue;  // n_pack is a multiple of 16: n < n_pack covers n + 3
+      const f32x4_t v = tot[b][r];
+      *reinterpret_cast<uint2*>(a.out + (long long)t * a.n_pack + n) =
+          make_uint2(pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3]));
+    }
+  }
+}
+
 struct RCfg {
   int tb, rb, r;
 };
 
-// Tile configuration by batch size (it does not change any logit's bits). Measured per
-// call at H=2048, n_pack=320 (8 launches graph-replayed): T <= 128 (1,1,4) 6.1-6.2 µs;
-// 256 (2,1,8) 9.3; 512 (2,2,4) 11.4; 1024 (4,2,4) 15.9; 2048 (4,4,4) 21.1; 4096 (4,4,2)
-// 39.7. MOE_ROUTER_CFG "tb,rb,r" overrides it (tuning knob).
+// Tile configuration of the split kernel by batch size (it does not change any logit's
+// bits). Measured per call at H=2048, n_pack=320 (8 launches graph-replayed): T <= 128
+// (1,1,4) 6.1-6.2 µs; 256 (2,1,8) 9.3; 512 (2,2,4) 11.4; 1024 (4,2,4) 15.9 (the tiled
+// kernel, 128-k chunks: 14.7 from ~1k tokens; 20.5 at 4096 against 39.7 here).
+// MOE_ROUTER_CFG "tb,rb,r" overrides it (tuning knob).
 RCfg router_cfg(int T) {
   const char* env = getenv("MOE_ROUTER_CFG");
   RCfg c{};
@@ -170,7 +289,6 @@ hipError_t launch_router_gemm(const void* x, int T, int H, const void* w_pack, i
                               void* logits, hipStream_t st) {
   if (!router_gemm_fits(H, n_pack)) return hipErrorInvalidValue;
   if (T <= 0) return hipSuccess;
-  const RCfg c = router_cfg(T);
   RouterArgs a{};
   a.x = static_cast<const uint16_t*>(x);
   a.w = static_cast<const uint16_t*>(w_pack);
@@ -178,6 +296,25 @@ hipError_t launch_router_gemm(const void* x, int T, int H, const void* w_pack, i
   a.T = T;
   a.H = H;
   a.n_pack = n_pack;
+  const char* env_tiles = getenv("MOE_ROUTER_TILES");  // token count from which the tiles run
+  const int tiles_from = env_tiles ? atoi(env_tiles) : kRouterTilesFrom;
+  const char* env_kc = getenv("MOE_ROUTER_TILE_K");
+  const int kc = env_kc && atoi(env_kc) == 64 ? 64 : 128;
+  if (T >= tiles_from && H % (kRouterSplit * kc) == 0) {
+    a.ntiles = (T + kTT - 1) / kTT;
+    a.nrg = (n_pack + kTN - 1) / kTN;
+    a.xcd_map = a.ntiles >= kXcdsR;
+    const long long grid = a.xcd_map
+                               ? (long long)((a.ntiles + kXcdsR - 1) / kXcdsR) * kXcdsR * a.nrg
+                               : (long long)a.ntiles * a.nrg;
+    if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
+    if (kc == 64)
+      hipLaunchKernelGGL(k_router_tiles<64>, dim3((unsigned)grid), dim3(256), 0, st, a);
+    else
+      hipLaunchKernelGGL(k_router_tiles<128>, dim3((unsigned)grid), dim3(256), 0, st, a);
+    return hipGetLastError();
+  }
+  const RCfg c = router_cfg(T);
   a.ntiles = (T + 16 * c.tb - 1) / (16 * c.tb);
   a.nrg = (n_pack + 16 * c.rb - 1) / (16 * c.rb);
   a.xcd_map = a.ntiles >= kXcdsR;

@@ -6,7 +6,11 @@ independent of the row count").
 Within one path (decode, tiled, prefill) the per-row arithmetic is fixed: the router's dot
 products, the top-k, each expert projection's K order and the combine are per token, so
 the comparison is bitwise. The router GEMM of the tiled and prefill paths sums every logit
-in one fixed order at every batch size, so the logits themselves are bitwise too. Across
+in one fixed order at every batch size (its small-batch and its tiled prefill kernels give
+the same bits: 1100 -> 900 and 2048 -> 100 cross from one to the other; 2048 -> 100 also
+crosses from the prefill GEMM tiles to the tiled expert GEMM, so there only the routing is
+bitwise), so the logits
+themselves are bitwise too. Across
 paths the fp32 summation order of a projection differs and only the bf16 tolerance applies
 (tested elsewhere)."""
 
@@ -33,7 +37,8 @@ def mlp(dev):
                                               (16, 5, False), (100, 64, False),
                                               (255, 17, False), (512, 300, False), (300, 129, False),
                                               (1536, 1024, False),
-                                              (4096, 2048, False)])
+                                              (4096, 2048, False), (1100, 900, False),
+                                              (2048, 100, False)])
 def test_leading_rows_match_smaller_batch(pkg, dev, mlp, big, small, decode):
     print(f"row independence {big} -> {small} decode={decode}", flush=True)
     g = torch.Generator().manual_seed(big + small)
@@ -45,4 +50,7 @@ def test_leading_rows_match_smaller_batch(pkg, dev, mlp, big, small, decode):
     torch.cuda.synchronize()
     assert torch.equal(la[:small], lb), "router logits depend on the batch"
     assert torch.equal(ia[:small], ib) and torch.equal(wa[:small], wb)
-    assert torch.equal(a[:small], b)
+    # the experts' GEMM path changes above 512 tokens (tiled -> prefill tiles), with its own
+    # fp32 summation order: across that boundary only the routing is compared
+    if (big > 512) == (small > 512):
+        assert torch.equal(a[:small], b)
