@@ -1,6 +1,6 @@
 """The block under HIP graph capture (how the engine runs decode, engine/fast/model.py:1947-2093):
 every regime — the three-launch decode path, the tiled decode path, fp8 experts with the bf16
-shared expert on the auxiliary stream, the prefill tiles with the hipBLASLt router — is
+shared expert on the auxiliary stream, the prefill tiles with the LDS-tiled router — is
 captured once and replayed several times with eager calls in between; every replay must give
 the eager call's bits."""
 
