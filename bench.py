@@ -183,17 +183,18 @@ def run_config(torch, dev, name, T, layers, steps, warmup, zipf=False, fp8=False
         ok = ok and bool(torch.isfinite(out.float()).all())
     torch.cuda.synchronize()
     D = sum(Ds) / len(Ds)
-    if name == "c2":
-        # the GPU result of layer 0 for the CPU leg's accuracy check (cpu_baseline)
-        mlp, x = mlps[0], xs[0]
-        out, idx, wts, logits = pkg.block.moe(x, mlp, K_TOP, decode=True, return_routing=True)
-        sh = mlp.shared_expert
-        _ACC_SAMPLE.update(
-            x=x.cpu(), out=out.cpu(), idx=idx.cpu(), wts=wts.cpu(), logits=logits.cpu(),
-            w={"router": mlp.gate.weight, "gate_up": mlp.experts.gate_up_proj,
-               "down": mlp.experts.down_proj, "sh_gate": sh.gate_proj.weight,
-               "sh_up": sh.up_proj.weight, "sh_down": sh.down_proj.weight,
-               "sh_gate_w": mlp.shared_expert_gate.weight})
+    # the GPU result of layer 0 for the CPU leg's accuracy check (cpu_baseline)
+    mlp, x = mlps[0], xs[0]
+    out, idx, wts, logits = pkg.block.moe(x, mlp, K_TOP, decode=T <= 64, return_routing=True)
+    sh, ex = mlp.shared_expert, mlp.experts
+    w0 = {"router": mlp.gate.weight, "gate_up": ex.gate_up_proj, "down": ex.down_proj,
+          "sh_gate": sh.gate_proj.weight, "sh_up": sh.up_proj.weight,
+          "sh_down": sh.down_proj.weight, "sh_gate_w": mlp.shared_expert_gate.weight}
+    if fp8:
+        w0.update(gate_up_scale=ex.gate_up_scale, down_scale=ex.down_scale)
+    _ACC_SAMPLE[name] = dict(x=x.cpu(), out=out.cpu(), idx=idx.cpu(), wts=wts.cpu(),
+                             logits=logits.cpu(), w=w0, fp8=fp8, decode=T <= 64)
+    del out, idx, wts, logits
 
     def calls(n):
         # n layer calls, cycling the L distinct layers
@@ -349,27 +350,33 @@ def cpu_baseline(torch, seconds):
             ts.append(time.perf_counter() - t1)
         ts.sort()
         others[name] = {"T": T, "us_per_layer": round(ts[len(ts) // 2] * 1e6, 1), "calls": len(ts)}
-    acc = None
-    if _ACC_SAMPLE:
-        # the same check the parity tests make, on the bench's own C2 layer 0: the GPU output
-        # and the reference torch path (batched_mm rounding) against the fp32 oracle
-        sm = _ACC_SAMPLE
+    acc = {}
+    for name, sm in _ACC_SAMPLE.items():
+        # the same check the parity tests make, on each config's own layer 0: the GPU output
+        # and (bf16 experts) the reference torch path on the same routing against the fp32
+        # oracle; fp8 experts against the oracle on the dequantised weights
         lg = sm["logits"][:, :E].float()
         f32 = orc.block_fp32(sm["x"], sm["w"], sm["idx"], logits=lg)
-        wc, ic = orc.compact_experts(sm["w"], sm["idx"])
-        ref = orc.block_bf16_routed(sm["x"], wc, ic, sm["wts"], sm["logits"][:, E:E + 1],
-                                    decode=True)
 
         def mrel(a, b):
             return float((a.float() - b).abs().mean() / b.abs().mean())
 
-        acc = {"max_abs_vs_fp32": round(float((sm["out"].float() - f32).abs().max()), 6),
-               "mean_rel_vs_fp32": round(mrel(sm["out"], f32), 6),
-               "mean_rel_ref_path_vs_fp32": round(mrel(ref, f32), 6),
-               "bar": "max-abs 2e-2; mean-rel 5e-3, or 1.1x the reference path's own "
-                      "mean-rel where that exceeds 5e-3 (its bf16 rounding points alone do)"}
+        a = {"tokens": int(sm["x"].shape[0]),
+             "max_abs_vs_fp32": round(float((sm["out"].float() - f32).abs().max()), 6),
+             "mean_rel_vs_fp32": round(mrel(sm["out"], f32), 6)}
+        if sm["fp8"]:
+            a["bar"] = "fp8 experts against the fp32 oracle on the dequantised weights: " \
+                       "max-abs 2e-2, mean-rel 6e-3"
+        else:
+            wc, ic = orc.compact_experts(sm["w"], sm["idx"])
+            ref = orc.block_bf16_routed(sm["x"], wc, ic, sm["wts"], sm["logits"][:, E:E + 1],
+                                        decode=sm["decode"])
+            a["mean_rel_ref_path_vs_fp32"] = round(mrel(ref, f32), 6)
+            a["bar"] = "max-abs 2e-2; mean-rel 5e-3, or 1.1x the reference path's own " \
+                       "mean-rel where that exceeds 5e-3 (its bf16 rounding points alone do)"
+        acc[name] = a
     return {
-        "accuracy_c2": acc,
+        "accuracy": acc or None,
         "value": round(med * 1e6, 1), "unit": "us/layer", "cores": torch.get_num_threads(),
         "affinity_cores": len(os.sched_getaffinity(0)), "kind": "port",
         "sample": f"C2 decode batch 1, {n} layer calls of the bf16 CPU torch path "
@@ -535,7 +542,7 @@ def main():
         raise SystemExit("bench.py: --configs needs at least one of c2, c3, c4, c5")
     head = workloads.get("c2") or next(iter(workloads.values()))
     cpu = None if args.no_cpu else cpu_baseline(torch, args.cpu_seconds)
-    accuracy = cpu.pop("accuracy_c2", None) if cpu else None
+    accuracy = cpu.pop("accuracy", None) if cpu else None
     kbytes, kus = head["gate_up_bytes"], head["gate_up_us"]
     achieved = kbytes / (kus * 1e-6) / 1e9
     traffic = measured_traffic(head["gate_up_kernel"], head_name(workloads))
@@ -565,7 +572,7 @@ def main():
                      "traffic_source": traffic["source"] if traffic else None,
                      "bytes_per_launch": kbytes, "us_per_launch": kus},
         "cpu_baseline": cpu,
-        "accuracy_c2": accuracy,
+        "accuracy": accuracy,
         "configs": results,
     }
     print(json.dumps(line), flush=True)
