@@ -136,3 +136,23 @@ def test_decode_fits_only_instantiated_hidden_sizes(pkg, H, fits):
     """The decode kernels are instantiated for H = 512 x {1, 2, 4, 8}; other multiples of
     512 go to the tiled path instead of failing at launch."""
     assert pkg._lib.load().moe_decode_fits(1, H, 256, 8, 512, 512) == fits
+
+
+def test_noalloc_rejects_calls_beyond_its_scratch_before_any_launch(pkg):
+    """moe_block_forward_noalloc checks the call's workspace against the static scratch
+    (MOE_NOALLOC_SCRATCH_BYTES) before touching the GPU: too many tokens fail with MOE_EINVAL
+    and a message naming the limit; the header's size and the Python constant agree."""
+    lib = pkg._lib.load()
+    hdr = (ROOT / "include" / "moe_mi355x.h").read_text()
+    assert re.search(r"#define MOE_NOALLOC_SCRATCH_BYTES \(16u << 20\)", hdr)
+    H, E, K, I, NP = 2048, 256, 8, 512, 320
+    T = 1
+    while lib.moe_block_workspace_bytes(T, H, E, K, I, I, NP) <= pkg._lib.NOALLOC_SCRATCH_BYTES:
+        T *= 2
+    rc = lib.moe_block_forward_noalloc(None, T, H, E, K, I, I, None, NP, None, None, None, None,
+                                       0, None, None, None, None, 0, None, None, None, None, None)
+    assert rc == pkg._lib.MOE_EINVAL
+    assert b"static scratch" in lib.moe_last_error()
+    rc = lib.moe_block_forward_noalloc(None, -1, H, E, K, I, I, None, NP, None, None, None, None,
+                                       0, None, None, None, None, 0, None, None, None, None, None)
+    assert rc == pkg._lib.MOE_EINVAL
