@@ -357,6 +357,175 @@ __global__ __launch_bounds__(64 * kGuWaves) void k_dec_gate_up(DecodeArgs a) {
   }
 }
 
+// K2 for three or four tokens: each routed workgroup routes once and then takes G
+// consecutive blocks of kGuWaves gate/up row pairs of its expert, requesting the rows of
+// block g + 1 before multiplying block g (one routing and one round of workgroups instead
+// of G: at four tokens the one-block kernel needs 5.5 rounds of resident workgroups, each
+// paying the routing before its first weight request). The token rows are staged in LDS
+// once per workgroup (read by its four waves and all G blocks) instead of being loaded by
+// every wave: at four tokens the per-wave copies were twice the bytes of the weight rows
+// and held 64 registers through the routing. Same dot products in the same order as
+// k_dec_gate_up. grid: [IS / kGuWaves shared row blocks] + P slots x (I / kGuWaves / G)
+// row-block groups.
+template <int NT, int HC, bool FP8, int EPL, int G>
+__global__ __launch_bounds__(64 * kGuWaves)
+__attribute__((amdgpu_waves_per_eu(HC <= 4 ? 4 : 1))) void k_dec_gate_up_multi(DecodeArgs a) {
+  static_assert(NT > 1 && NT <= kGuWaves, "one token routed per wave");
+  constexpr int kRowU4 = HC * 64;        // 16-byte units of one token row
+  __shared__ int s_idx[64];
+  __shared__ uint4 s_x[NT * kRowU4];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int H = HC * 512;
+  const int P = a.T * a.k;
+  const int ngrp = a.I / kGuWaves / G;   // routed workgroups per slot
+  const int nsh = a.sh_in_gate_up && a.sh_gate ? a.IS / kGuWaves : 0;
+
+  if ((int)blockIdx.x < nsh) {
+    // shared gate/up row pair n: no routing dependency (as in k_dec_gate_up)
+    uint4 xv[NT][HC];
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int c = 0; c < HC; ++c)
+        xv[t][c] = ld16(a.x + (long long)min(t, a.T - 1) * H + c * 512 + lane * 8);
+    const int n = blockIdx.x * kGuWaves + wave;
+    const uint16_t* rg = a.sh_gate + (long long)n * H;
+    const uint16_t* ru = a.sh_up + (long long)n * H;
+    uint4 wg[HC], wu[HC];
+#pragma unroll
+    for (int c = 0; c < HC; ++c) wg[c] = ld16_stream(rg + c * 512 + lane * 8);
+#pragma unroll
+    for (int c = 0; c < HC; ++c) wu[c] = ld16_stream(ru + c * 512 + lane * 8);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      float sg = 0.f, su = 0.f;
+#pragma unroll
+      for (int c = 0; c < HC; ++c) {
+        sg = dot8(wg[c], xv[t][c], sg);
+        su = dot8(wu[c], xv[t][c], su);
+      }
+      sg = wave_sum(sg);
+      su = wave_sum(su);
+      if (lane == 0 && t < a.T) a.act_sh[(long long)t * a.IS + n] = f2bf_bits(swiglu(sg, su));
+    }
+    return;
+  }
+  const int bid = blockIdx.x - nsh;
+  const int slot = bid / ngrp;
+  const int blk0 = (bid - slot * ngrp) * G;  // first row block of this workgroup
+
+  // token rows into registers now (independent of the routing), into LDS after it
+  constexpr int kXUnits = NT * kRowU4;
+  constexpr int kXPer = (kXUnits + 64 * kGuWaves - 1) / (64 * kGuWaves);  // per thread
+  uint4 xs[kXPer];
+#pragma unroll
+  for (int i = 0; i < kXPer; ++i) {
+    const int u = threadIdx.x + i * 64 * kGuWaves;
+    const int t = u / kRowU4;
+    if (u < kXUnits)
+      xs[i] = reinterpret_cast<const uint4*>(a.x + (long long)min(t, a.T - 1) * H)[u - t * kRowU4];
+  }
+
+  // routing: wave t routes token t; key of lane p = the expert of pair p (lanes < P)
+  if (a.logits) {
+    if (wave < a.T) {
+      int my_idx;
+      float my_w;
+      route_row<EPL>(a.logits + (long long)wave * a.n_pack, a.E, a.k, lane, my_idx, my_w);
+      if (lane < a.k) {
+        const int p = wave * a.k + lane;
+        s_idx[p] = my_idx;
+        if (bid == 0) {
+          a.idx32[p] = my_idx;
+          a.wts[p] = f2bf_bits(my_w);
+          if (a.idx64) a.idx64[p] = my_idx;
+        }
+      }
+    }
+  } else if (threadIdx.x < P) {
+    const long long v = a.ids_in[threadIdx.x];
+    const int ev = (int)(v < 0 ? 0 : (v >= a.E ? a.E - 1 : v));
+    s_idx[threadIdx.x] = ev;
+    if (bid == 0) a.idx32[threadIdx.x] = ev;
+  }
+#pragma unroll
+  for (int i = 0; i < kXPer; ++i)
+    if (threadIdx.x + i * 64 * kGuWaves < kXUnits) s_x[threadIdx.x + i * 64 * kGuWaves] = xs[i];
+  __syncthreads();
+  const int key = lane < P ? s_idx[lane] : -1;
+  // distinct experts numbered in first-use order (pair order)
+  bool first = lane < P;
+  for (int q = 0; q < P; ++q) {
+    const int kq = __builtin_amdgcn_readlane(key, q);
+    if (q < lane && kq == key) first = false;
+  }
+  const unsigned long long fmask = __ballot(first);
+  const int rank = __popcll(fmask & ((1ull << lane) - 1ull));
+  if (slot >= __popcll(fmask)) return;
+  const unsigned long long smask = __ballot(first && rank == slot);
+  const int e = __builtin_amdgcn_readlane(key, __ffsll((long long)smask) - 1);
+  const unsigned long long pmask0 = __ballot(lane < P && key == e);
+  const long long base = (long long)e * 2 * a.I;
+
+  WFrag<FP8> fg[2][HC], fu[2][HC];
+  float scg[2] = {1.f, 1.f}, scu[2] = {1.f, 1.f};
+  auto request = [&](int buf, int n) __attribute__((always_inline)) {
+    if (a.gu_scale) {
+      scg[buf] = a.gu_scale[base + n];
+      scu[buf] = a.gu_scale[base + a.I + n];
+    }
+    const void* rg = wrow<FP8>(a.gate_up, base + n, H);
+    const void* ru = wrow<FP8>(a.gate_up, base + a.I + n, H);
+#pragma unroll
+    for (int c = 0; c < HC; ++c) {
+      fg[buf][c] = ldraw<FP8>(rg, c * 512 + lane * 8);
+      fu[buf][c] = ldraw<FP8>(ru, c * 512 + lane * 8);
+    }
+  };
+  request(0, blk0 * kGuWaves + wave);
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const int b = g & 1;
+    const int n = (blk0 + g) * kGuWaves + wave;
+    if (g + 1 < G) request(b ^ 1, (blk0 + g + 1) * kGuWaves + wave);
+    float sg[NT], su[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) sg[t] = su[t] = 0.f;
+#pragma unroll
+    for (int c = 0; c < HC; ++c) {
+      const uint4 wg = decode<FP8>(fg[b][c]);
+      const uint4 wu = decode<FP8>(fu[b][c]);
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const uint4 xv = s_x[t * kRowU4 + c * 64 + lane];
+        sg[t] = dot8(wg, xv, sg[t]);
+        su[t] = dot8(wu, xv, su[t]);
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      sg[t] = wave_sum(sg[t]) * scg[b];
+      su[t] = wave_sum(su[t]) * scu[b];
+    }
+    // lane 0 writes each pair of this expert (at most one per token)
+    unsigned long long pmask = pmask0;
+    while (pmask) {
+      const int p = __ffsll((long long)pmask) - 1;
+      pmask &= pmask - 1;
+      const int t = p / a.k;
+      float gg = sg[0], uu = su[0];
+#pragma unroll
+      for (int tt = 1; tt < NT; ++tt)
+        if (t == tt) {
+          gg = sg[tt];
+          uu = su[tt];
+        }
+      if (lane == 0) a.act[(long long)p * a.I + n] = f2bf_bits(swiglu(gg, uu));
+    }
+  }
+}
+
 // ------------------------------------------------------------------------------- K3
 
 // grid: H / 4 workgroups; wave w computes hidden row 4 * blockIdx.x + w of every token.
@@ -551,6 +720,14 @@ bool decode_fits(const DecodeArgs& a) {
 
 namespace {
 
+// Row blocks per routed K2 workgroup at three or four tokens: MOE_DECODE_GU_BLOCKS=1, 2
+// or 4 (comparisons; 1 is the one-block kernel that loads the token rows per wave).
+int gate_up_blocks() {
+  const char* env = getenv("MOE_DECODE_GU_BLOCKS");
+  const int v = env ? atoi(env) : 4;
+  return v == 1 || v == 2 ? v : 4;
+}
+
 // MOE_DECODE_DOWN=rows: the wave-per-row down kernel for one token too (comparisons).
 bool down_legacy() {
   const char* env = getenv("MOE_DECODE_DOWN");
@@ -575,12 +752,22 @@ hipError_t launch_router_nt(const DecodeArgs& a, hipStream_t s) {
 
 template <int NT, bool FP8>
 hipError_t launch_gate_up_nt(const DecodeArgs& a, hipStream_t s) {
-  const int grid =
-      a.T * a.k * (a.I / kGuWaves) + (a.sh_gate && a.sh_in_gate_up ? a.IS / kGuWaves : 0);
+  // three or four tokens: G row blocks per routed workgroup (I / kGuWaves is a multiple of 4)
+  const int G = NT == 4 ? gate_up_blocks() : 1;
+  const bool multi = G > 1;
+  const int grid = a.T * a.k * (a.I / kGuWaves / G) +
+                   (a.sh_gate && a.sh_in_gate_up ? a.IS / kGuWaves : 0);
   const int epl = a.logits ? (a.E + 63) / 64 : 1;
 #define LG(HC, EPL)                                                                         \
   if (a.H / 512 == HC && epl <= EPL) {                                                      \
-    hipLaunchKernelGGL((k_dec_gate_up<NT, HC, FP8, EPL>), dim3(grid), dim3(64 * kGuWaves), 0, s, a); \
+    if (multi && G == 4)                                                                    \
+      hipLaunchKernelGGL((k_dec_gate_up_multi<4, HC, FP8, EPL, 4>), dim3(grid),             \
+                         dim3(64 * kGuWaves), 0, s, a);                                     \
+    else if (multi)                                                                         \
+      hipLaunchKernelGGL((k_dec_gate_up_multi<4, HC, FP8, EPL, 2>), dim3(grid),             \
+                         dim3(64 * kGuWaves), 0, s, a);                                     \
+    else                                                                                    \
+      hipLaunchKernelGGL((k_dec_gate_up<NT, HC, FP8, EPL>), dim3(grid), dim3(64 * kGuWaves), 0, s, a); \
     return hipGetLastError();                                                               \
   }
 #define LH(HC) LG(HC, 1) LG(HC, 2) LG(HC, 4) LG(HC, 8)

@@ -211,6 +211,41 @@ def test_decode_one_token_down_kernels_agree(pkg, dev, layer, fp8):
     assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("T", [3, 4])
+@pytest.mark.parametrize("routes", ["random", "shared_experts"])
+def test_decode_gate_up_row_blocks_agree(pkg, dev, layer, T, routes):
+    """Three or four tokens: the gate_up kernel that takes four row blocks per workgroup
+    (token rows staged in LDS) and the one-block kernel compute the same dot products in
+    the same order, so the block's outputs and routing agree bit for bit, also when tokens
+    share experts (one workgroup then serves several pairs)."""
+    mlp = _mlp(layer, dev)
+    g = torch.Generator().manual_seed(90 + T)
+    x = torch.randn(T, 2048, generator=g)
+    if routes == "shared_experts":
+        x[1:] = x[0] + 0.05 * x[1:]  # near-identical tokens: mostly the same experts
+    x = x.to(BF16).to(dev)
+    r = torch.randn(T, 2048, generator=g).to(BF16).to(dev)
+    got = {}
+    old = os.environ.get("MOE_DECODE_GU_BLOCKS")
+    try:
+        for blocks in ("4", "2", "1"):
+            os.environ["MOE_DECODE_GU_BLOCKS"] = blocks
+            got[blocks] = pkg.block.moe(x, mlp, 8, decode=True, residual=r, return_routing=True)
+    finally:
+        if old is None:
+            os.environ.pop("MOE_DECODE_GU_BLOCKS", None)
+        else:
+            os.environ["MOE_DECODE_GU_BLOCKS"] = old
+    torch.cuda.synchronize()
+    distinct = int(torch.unique(got["1"][1]).numel())
+    _say(f"decode gate_up row blocks T={T} {routes}: {distinct} distinct experts")
+    if routes == "shared_experts":
+        assert distinct < T * 8
+    for blocks in ("4", "2"):
+        for a, b in zip(got[blocks], got["1"]):
+            assert torch.equal(a, b), blocks
+
+
 @pytest.mark.parametrize("E,k", [(256, 8), (64, 8), (16, 4)])
 def test_decode_gate_up_hard_routing_rows(pkg, dev, E, k):
     """One token per call on rows built to need the exact-selection fallback (p ties from
