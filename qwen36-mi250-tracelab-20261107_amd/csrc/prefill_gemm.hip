@@ -137,12 +137,19 @@ __global__ __launch_bounds__(kThreads, 1) void k_prefill_gemm(GemmArgs args) {
   const int nrb = args.nrb;
   const int xcd = blockIdx.x & (kXcds - 1);
   const int j = blockIdx.x / kXcds;
-  const int tile = (j / nrb) * kXcds + xcd;
+  int tile = (j / nrb) * kXcds + xcd;
   const int rb = j - (j / nrb) * nrb;
   if (tile >= args.MTgrid) return;
   int e, r0, r1;
   if (args.table) {
-    if (tile >= args.table[3 * args.MT]) return;
+    const int ntiles = args.table[3 * args.MT];
+    if (tile >= ntiles) return;
+    if (args.shared_first > 0) {
+      // the shared expert's tiles (the table's last ones, whole 256-token tiles, the longest
+      // workgroups) are dispatched first, the routed tiles fill in behind them
+      const int ns = min(args.shared_first, ntiles);
+      tile = tile < ns ? ntiles - ns + tile : tile - ns;
+    }
     e = args.table[tile];
     r0 = args.table[args.MT + tile];
     // the table holds the expert's end row; this tile is its next PBM rows at most (the
@@ -354,6 +361,11 @@ hipError_t launch_prefill_gemm(int mode, const GemmArgs& a_in, int max_tiles, hi
   if (a.nrb <= 0 || max_tiles <= 0) return hipSuccess;
   const size_t lds = (size_t)kLdsBytes;
   a.MTgrid = max_tiles;
+  a.shared_first = 0;
+  if (a.table && a.op[0].N > 0 && a.op[1].N > 0) {
+    const char* env = getenv("MOE_PREFILL_SHARED_FIRST");
+    if (!(env && env[0] == '0')) a.shared_first = (a.T + PBM - 1) / PBM;
+  }
   const long long grid = (long long)((max_tiles + kXcds - 1) / kXcds) * kXcds * a.nrb;
   const void* fn = mode == kModeSwiglu
                        ? reinterpret_cast<const void*>(&k_prefill_gemm<kModeSwiglu>)

@@ -465,3 +465,41 @@ def test_block_shape_sweep(pkg, dev, H, E, K, I, IS, T):
     _say(f" vs fp32 max {max_abs(out, f32):.3g} mean-rel {ours:.3g} (reference path {theirs:.3g})")
     assert max_abs(out, f32) <= 2e-2
     assert ours <= max(5e-3, 1.1 * theirs)
+
+
+@pytest.mark.parametrize("T", [600, 1500])
+def test_prefill_shared_tile_order_and_side_launch_agree(pkg, dev, full_layer, T):
+    """A grouped prefill launch holding routed and shared tiles gives the same bits whether
+    the shared expert's tiles are dispatched first (default), in table order, or run as a
+    second launch on the auxiliary stream: every tile is computed the same way, only the
+    order and the queue differ. Checked for gate_up and down."""
+    import os
+
+    w, _ = full_layer
+    g = torch.Generator().manual_seed(T + 5)
+    x = torch.randn(T, 2048, generator=g).to(BF16).to(dev)
+    logits = pkg.ops.router_logits(x, w["router"])
+    _, idx, _ = pkg.ops.route(logits, 8, experts=256)
+    sp = pkg.ops.sort_pairs(idx, 256, shared=True)
+    runs = {}
+    saved = {k: os.environ.get(k) for k in ("MOE_PREFILL_SIDE", "MOE_PREFILL_SHARED_FIRST")}
+    try:
+        for name, env in (("first", {}), ("table", {"MOE_PREFILL_SHARED_FIRST": "0"}),
+                          ("side", {"MOE_PREFILL_SIDE": "1"})):
+            for k in saved:
+                os.environ.pop(k, None)
+            os.environ.update(env)
+            act, act_sh = pkg.ops.grouped_gate_up(x, 8, w["gate_up"], sp,
+                                                  shared=(w["sh_gate"], w["sh_up"]))
+            y, y_sh = pkg.ops.grouped_down(act, T, 8, w["down"], sp, shared=(w["sh_down"], act_sh))
+            torch.cuda.synchronize()
+            runs[name] = (act.clone(), act_sh.clone(), y.clone(), y_sh.clone())
+    finally:
+        for k, v in saved.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+    for name in ("table", "side"):
+        for a, b in zip(runs["first"], runs[name]):
+            assert torch.equal(a, b), name
