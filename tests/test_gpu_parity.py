@@ -177,10 +177,13 @@ def test_experts_forward_matches_oracle(pkg, dev, n, mode, shape):
 
 @pytest.mark.parametrize("n", [600, 1500])
 @pytest.mark.parametrize("mode", ["uniform", "skewed", "one"])
-def test_experts_prefill_tiles_match_oracle(pkg, dev, n, mode):
-    """More than 512 tokens: the 256-row prefill GEMM tiles (H % 256 == 0, I % 128 == 0)."""
-    e, h, i, k = 32, 256, 128, 8
-    _say("experts prefill", n, mode)
+@pytest.mark.parametrize("shape", [(32, 256, 128, 8), (16, 2048, 1024, 4)])
+def test_experts_prefill_tiles_match_oracle(pkg, dev, n, mode, shape):
+    """More than 512 tokens: the 256-row prefill GEMM tiles (H % 256 == 0, I % 128 == 0), at
+    a small shape and at the model's hidden size with a doubled intermediate (32 / 16 DMA
+    chunks per gate_up / down workgroup)."""
+    e, h, i, k = shape
+    _say("experts prefill", n, mode, shape)
     assert pkg._lib.load().moe_tile_rows(n) == 256
     m = _Experts(e, h, i, seed=n)
     g = torch.Generator().manual_seed(n + 2)
