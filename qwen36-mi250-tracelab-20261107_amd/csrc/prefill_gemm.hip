@@ -31,6 +31,7 @@
 
 #include "moe_common.h"
 #include "expert_gemm.h"
+#include "lds_dma.h"
 
 namespace moe {
 
@@ -57,25 +58,6 @@ constexpr int kLoadsPerWave = kGroups / (kThreads / 64);  // per operand and chu
 static_assert(kLoadsPerWave == 4, "wait_loads counts 4 loads per operand per chunk");
 static_assert(kAheadA <= kStagesA - 1 && kAheadB <= kStagesB - 1, "ring slots reused early");
 }  // namespace
-
-typedef unsigned u32x4v __attribute__((ext_vector_type(4)));
-
-template <int OFF>
-__device__ __forceinline__ u32x4v lds_read_frag(uint32_t addr) {
-  u32x4v r;
-  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
-  return r;
-}
-__device__ __forceinline__ void lds_frags_ready() {
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-}
-// Ties a fragment to the wait above: its users cannot move before it.
-__device__ __forceinline__ void after_wait(u32x4v& v) { asm volatile("" : "+v"(v)); }
-
-__device__ __forceinline__ f32x4_t mfma_frag(u32x4v a, u32x4v b, f32x4_t c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
-                                                 __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
-}
 
 // MFMA fragments of one chunk for a wave: 4 weight-row blocks, 8 token blocks.
 struct Frags {
@@ -115,20 +97,6 @@ __device__ __forceinline__ void mma_frags(const Frags& f, int nb, f32x4_t (&acc)
     if (b >= nb) break;
 #pragma unroll
     for (int a = 0; a < 4; ++a) acc[a][b] = mfma_frag(f.a[a], f.b[b], acc[a][b]);
-  }
-}
-
-// Wait until at most n (0..12) of this wave's DMA loads are still in flight.
-__device__ __forceinline__ void wait_loads(int n) {
-  switch (n) {
-#define W(N)                                          \
-  case N:                                             \
-    asm volatile("s_waitcnt vmcnt(" #N ")" ::: "memory"); \
-    break;
-    W(12) W(11) W(10) W(9) W(8) W(7) W(6) W(5) W(4) W(3) W(2) W(1)
-#undef W
-    default:
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   }
 }
 

@@ -22,12 +22,18 @@
 //   whole K, restarting its accumulator at every quarter and folding it into a running
 //   total, which reproduces ((s0 + s1) + s2) + s3 bit for bit with a quarter of the operand
 //   traffic of the split kernel.
+// * k_router_dma: the same tiles and order with the operands staged by global -> LDS DMA
+//   (the default from 768 tokens: 16.1 against 20.7 µs at 4096 tokens, 12.7 against 14.8
+//   at 768; k_router_tiles remains for MOE_ROUTER_DMA=0).
 // Workgroups of one token tile get ids 8 apart so they run on one XCD and share the tile's
 // token rows in its L2 (the router rows, 1.25 MiB, stay in every XCD's L2).
 #include <stdio.h>
 #include <stdlib.h>
 
+#include <mutex>
+
 #include "moe_common.h"
+#include "lds_dma.h"
 
 namespace moe {
 
@@ -260,6 +266,125 @@ __global__ __launch_bounds__(256) void k_router_tiles(RouterArgs a) {
   }
 }
 
+// The same tile and summation order with the chunks staged by global -> LDS DMA
+// (global_load_lds_dwordx4: no registers on the way, more bytes in flight per CU) in a ring
+// of S stages, chunk d + S - 1 requested while chunk d is multiplied. Wave w's DMA load i
+// fills the 4-row group w + 4 i of a stage (1 KiB: 4 rows x 256 bytes), lane l writing
+// physical unit l & 15 of row l >> 4 of the group with logical unit (l & 15) ^ (row & 15):
+// the layout k_router_tiles writes, so the fragment reads are the same. Fragments are read
+// by inline asm with explicit waits (lds_dma.h). Bit-identical to k_router_tiles.
+template <int S>
+__global__ __launch_bounds__(256) void k_router_dma(RouterArgs a) {
+  constexpr int KC = 128;                       // k per chunk: 256 bytes of each row
+  constexpr int kUnits = KC / 8;                // 16-byte units per staged row
+  constexpr int kRowBytes = KC * 2;
+  constexpr int kStage = kTRows * kRowBytes;    // 32 KiB
+  constexpr int kGroups = kTRows / 4;           // 4-row DMA groups per chunk: 32
+  constexpr int kLoads = kGroups / 4;           // per wave and chunk: 8
+  static_assert(kLoads * 4 == kGroups && (kLoads * (S - 2)) <= 12, "wait_loads range");
+  extern __shared__ uint4 smem[];
+  int tile, rg;
+  if (a.xcd_map) {
+    const int xcd = blockIdx.x & (kXcdsR - 1);
+    const int j = blockIdx.x / kXcdsR;
+    tile = (j / a.nrg) * kXcdsR + xcd;
+    rg = j - (j / a.nrg) * a.nrg;
+    if (tile >= a.ntiles) return;
+  } else {
+    tile = blockIdx.x / a.nrg;
+    rg = blockIdx.x - tile * a.nrg;
+  }
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wt = wave & 1, wn = wave >> 1;
+  const int lr = lane & 15, kq = lane >> 4;
+  const int t0 = tile * kTT, n0 = rg * kTN;
+
+  // DMA sources: group g = wave + 4 i, row 4 g + (lane >> 4) (tokens, then router rows)
+  const uint16_t* src[kLoads];
+#pragma unroll
+  for (int i = 0; i < kLoads; ++i) {
+    const int row = (wave + 4 * i) * 4 + (lane >> 4);
+    const int lu = (lane & 15) ^ (row & (kUnits - 1));
+    src[i] = row < kTT ? a.x + (long long)min(t0 + row, a.T - 1) * a.H + lu * 8
+                       : a.w + (long long)min(n0 + row - kTT, a.n_pack - 1) * a.H + lu * 8;
+  }
+  char* lds = reinterpret_cast<char*>(smem);
+  auto issue = [&](int d) __attribute__((always_inline)) {
+    char* st = lds + (d % S) * kStage;
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i)
+      __builtin_amdgcn_global_load_lds(src[i] + d * KC, st + (wave + 4 * i) * 1024, 16, 0, 0);
+  };
+  const uint32_t lbase = lds_addr(lds);
+  // this lane's fragment rows: router rows wn * 32 + r * 16 + lr, tokens wt * 32 + b * 16 + lr
+  const uint32_t arow0 = (uint32_t)((kTT + wn * 32 + lr) * kRowBytes);
+  const uint32_t brow0 = (uint32_t)((wt * 32 + lr) * kRowBytes);
+
+  f32x4_t acc[2][2], tot[2][2];  // [token block][row block]
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int r = 0; r < 2; ++r) acc[b][r] = tot[b][r] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  const int nd = a.H / KC;
+  const int per_q = nd / kRouterSplit;
+#pragma unroll
+  for (int c = 0; c < S - 1; ++c)
+    if (c < nd) issue(c);
+  for (int d = 0; d < nd; ++d) {
+    // chunk d: younger than it are chunks d + 1 .. d + S - 2 where issued
+    wait_loads(kLoads * max(0, min(S - 2, nd - 1 - d)));
+    __builtin_amdgcn_s_barrier();  // chunk d visible; the slot of chunk d - 1 free
+    if (d + S - 1 < nd) issue(d + S - 1);
+    const uint32_t st = lbase + (d % S) * kStage;
+#pragma unroll
+    for (int h = 0; h < KC / 32; ++h) {
+      // logical unit h * 4 + kq of each row, at its physical position
+      const uint32_t ua = (uint32_t)((((h * 4 + kq) ^ (lr & (kUnits - 1)))) * 16);
+      u32x4v fa[2], fb[2];
+      fa[0] = lds_read_frag<0>(st + arow0 + ua);
+      fa[1] = lds_read_frag<16 * kRowBytes>(st + arow0 + ua);
+      fb[0] = lds_read_frag<0>(st + brow0 + ua);
+      fb[1] = lds_read_frag<16 * kRowBytes>(st + brow0 + ua);
+      lds_frags_ready();
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        after_wait(fa[i]);
+        after_wait(fb[i]);
+      }
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int r = 0; r < 2; ++r) acc[b][r] = mfma_frag(fa[r], fb[b], acc[b][r]);
+    }
+    if ((d + 1) % per_q == 0) {  // end of a K quarter: total = ((s0 + s1) + s2) + s3
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+          tot[b][r] = d + 1 == per_q ? acc[b][r] : tot[b][r] + acc[b][r];
+          acc[b][r] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        }
+    }
+  }
+  // lane (q = kq, j = lr) holds rows 4q .. 4q + 3 of token column j of each block
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    const int t = t0 + wt * 32 + b * 16 + lr;
+    if (t >= a.T) continue;
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int n = n0 + wn * 32 + r * 16 + 4 * kq;
+      if (n >= a.n_pack) continue;
+      const f32x4_t v = tot[b][r];
+      *reinterpret_cast<uint2*>(a.out + (long long)t * a.n_pack + n) =
+          make_uint2(pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3]));
+    }
+  }
+}
+
 struct RCfg {
   int tb, rb, r;
 };
@@ -308,6 +433,32 @@ hipError_t launch_router_gemm(const void* x, int T, int H, const void* w_pack, i
                                ? (long long)((a.ntiles + kXcdsR - 1) / kXcdsR) * kXcdsR * a.nrg
                                : (long long)a.ntiles * a.nrg;
     if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
+    const char* env_dma = getenv("MOE_ROUTER_DMA");  // stages of the DMA kernel; 0: off
+    const int stages = env_dma ? atoi(env_dma) : 2;
+    if (kc == 128 && (stages == 2 || stages == 3)) {
+      const int bytes = stages * kTRows * 256;
+      const void* fn = stages == 3 ? reinterpret_cast<const void*>(&k_router_dma<3>)
+                                   : reinterpret_cast<const void*>(&k_router_dma<2>);
+      static std::mutex mu;
+      static uint64_t done[2] = {0, 0};  // bit d: device d, per stage count
+      int dev = 0;
+      hipError_t err = hipGetDevice(&dev);
+      if (err != hipSuccess) return err;
+      if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+      {
+        std::lock_guard<std::mutex> lock(mu);
+        if (!(done[stages - 2] >> dev & 1)) {
+          err = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+          if (err != hipSuccess) return err;
+          done[stages - 2] |= uint64_t(1) << dev;
+        }
+      }
+      if (stages == 3)
+        hipLaunchKernelGGL(k_router_dma<3>, dim3((unsigned)grid), dim3(256), bytes, st, a);
+      else
+        hipLaunchKernelGGL(k_router_dma<2>, dim3((unsigned)grid), dim3(256), bytes, st, a);
+      return hipGetLastError();
+    }
     if (kc == 64)
       hipLaunchKernelGGL(k_router_tiles<64>, dim3((unsigned)grid), dim3(256), 0, st, a);
     else
