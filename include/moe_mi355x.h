@@ -53,6 +53,14 @@ extern "C" {
 int moe_abi_version(void);
 const char* moe_last_error(void);
 
+/* Re-read the comparison switches from the environment (MOE_DECODE=0: no decode kernels;
+ * MOE_DECODE_DOWN=rows, MOE_DECODE_GU_BLOCKS=1|2|4, MOE_MIXED=0, MOE_PREFILL_SIDE=1,
+ * MOE_PREFILL_SHARED_FIRST=0: alternative launch structures with the same results). The
+ * library reads them once, at its first launch, and again only here, so no launch pays for
+ * them. No counterpart in the reference; for tests and comparisons. Not to be called while
+ * another thread launches through the library. */
+void moe_reload_tuning(void);
+
 /* Sorted rows per tile (bm) the fused entry points use for T tokens: 16 for one token,
  * 32 up to 512, above that 256 (the prefill tiles: bf16 weights, hidden a multiple of 256,
  * intermediates of 128) or else 64. A table passed to moe_grouped_gate_up /

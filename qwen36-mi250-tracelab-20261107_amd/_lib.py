@@ -35,6 +35,7 @@ _F = ctypes.c_float
 SIGNATURES: dict[str, tuple] = {
     "moe_abi_version": (_I, []),
     "moe_last_error": (ctypes.c_char_p, []),
+    "moe_reload_tuning": (None, []),
     "moe_tile_rows": (_I, [_I]),
     "moe_max_tiles": (_I, [_I, _I, _I, _I, _I]),
     "moe_router_logits": (_I, [_P, _I, _I, _P, _I, _P, _P]),

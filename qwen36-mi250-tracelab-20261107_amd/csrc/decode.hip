@@ -723,14 +723,14 @@ namespace {
 // Row blocks per routed K2 workgroup at three or four tokens: MOE_DECODE_GU_BLOCKS=1, 2
 // or 4 (comparisons; 1 is the one-block kernel that loads the token rows per wave).
 int gate_up_blocks() {
-  const char* env = getenv("MOE_DECODE_GU_BLOCKS");
+  const char* env = knob(kKnobDecodeGuBlocks);
   const int v = env ? atoi(env) : 4;
   return v == 1 || v == 2 ? v : 4;
 }
 
 // MOE_DECODE_DOWN=rows: the wave-per-row down kernel for one token too (comparisons).
 bool down_legacy() {
-  const char* env = getenv("MOE_DECODE_DOWN");
+  const char* env = knob(kKnobDecodeDown);
   return env && env[0] == 'r';
 }
 

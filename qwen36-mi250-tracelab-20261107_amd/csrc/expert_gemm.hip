@@ -401,26 +401,10 @@ bool fits(const Cfg& c, int mode, const GemmOperand& op) {
   return op.N % rows == 0 && op.K % (c.wk * c.kc) == 0;
 }
 
-// MOE_GEMM_CFG="router=wr,wk;gate_up=wr,wk;down=wr,wk" overrides the choice for a role
-// (tuning knob; read at each launch). TOKB follows from the tile rows.
-bool env_cfg(int role, Cfg* out) {
-  const char* env = getenv("MOE_GEMM_CFG");
-  if (!env) return false;
-  const char* names[] = {"router=", "gate_up=", "down="};
-  const char* p = strstr(env, names[role]);
-  if (!p) return false;
-  Cfg c{};
-  c.kc = 128;
-  c.r = 4;
-  if (sscanf(p + strlen(names[role]), "%d,%d,%d,%d", &c.wr, &c.wk, &c.kc, &c.r) < 2) return false;
-  *out = c;
-  return true;
-}
-
 }  // namespace
 
 bool mixed_enabled() {
-  const char* env = getenv("MOE_MIXED");
+  const char* env = knob(kKnobMixed);
   return !(env && env[0] == '0');
 }
 
@@ -438,11 +422,6 @@ hipError_t launch_expert_gemm(int mode, int role, int bm, const GemmArgs& a_in, 
   // few-token decode case); with 4 blocks, 4 row groups share the staged token rows.
   Cfg prefs[8];
   int n = 0;
-  Cfg forced;
-  if (env_cfg(role, &forced)) {
-    forced.tokb = tokb;
-    prefs[n++] = forced;
-  }
   // fp8 weights move half the bytes per K element: 128-element chunks keep as many bytes
   // in flight as the bf16 64-element ones.
   const int rr = fp8 ? 8 : 4;  // fp8: 64-element chunks are half the bytes, twice as many

@@ -7,6 +7,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <atomic>
 #include <mutex>
 #include <string>
 
@@ -41,11 +42,6 @@ namespace {
 // (K split over 4 waves), two blocks up to 512 tokens, and 256-row tiles of the prefill
 // kernel above (bf16 weights with shapes it tiles; else 64-row tiles of the expert GEMM).
 int tile_rows_for(int T, bool fp8 = false, int H = 2048, int I = 512, int IS = 512) {
-  const char* env = getenv("MOE_TILE_ROWS");
-  if (env) {
-    int v = atoi(env);
-    if (v == 16 || v == 32 || v == 64 || v == 128 || v == prefill_tile_rows()) return v;
-  }
   // 32-row tiles from 2 tokens: per layer (12 layers cycled) 8 / 16 tokens take 81 / 113 µs
   // with fp8 experts against 128 / 213 with 16-row tiles, and 102 / 150 against 107 / 166
   // with bf16; at 2 / 3 / 4 tokens (16 layers) fp8 50 / 53 / 56 against 55 / 68 / 79 and
@@ -87,7 +83,7 @@ int hip_check(hipError_t e, const char* what) {
 
 // The three-launch decode path (decode.hip) for T <= 4 unless MOE_DECODE=0.
 bool decode_enabled() {
-  const char* env = getenv("MOE_DECODE");
+  const char* env = knob(kKnobDecode);
   return !(env && env[0] == '0');
 }
 
@@ -103,28 +99,15 @@ bool decode_takes(int T, bool fp8) { return decode_enabled() && T <= (fp8 ? 2 : 
 // MOE_PREFILL_SIDE=1 restores the second launch. (The block forward runs the whole shared
 // expert on the auxiliary stream from its start instead; see block_side_enabled.)
 bool prefill_side_enabled() {
-  const char* env = getenv("MOE_PREFILL_SIDE");
+  const char* env = knob(kKnobPrefillSide);
   return env && env[0] == '1';
 }
 
-// Block forward: the shared expert on the auxiliary stream (MOE_BLOCK_SIDE=0 / 1 forces it
-// off / on; by default where it runs as separate launches anyway: fp8 routed experts or
-// prefill tiles).
-bool block_side_enabled(int T, bool fp8, int bm) {
-  const char* env = getenv("MOE_BLOCK_SIDE");
-  if (env) return env[0] == '1';
-  (void)T;
-  // fp8 routed experts: the shared expert's bf16 tiles share the routed launches
-  // (mixed_enabled) unless MOE_MIXED=0, which splits them onto the auxiliary stream
+// Block forward: the shared expert on the auxiliary stream where it runs as separate
+// launches anyway: fp8 routed experts whose bf16 shared tiles do not share the routed
+// launches (MOE_MIXED=0), or prefill tiles.
+bool block_side_enabled(bool fp8, int bm) {
   return (fp8 && !mixed_enabled()) || bm == prefill_tile_rows();
-}
-
-// Decode block: the shared expert's gate/up rows go to the gate_up launch, where they stream
-// while the routed workgroups route (MOE_DECODE_SHARED=router keeps them in the router
-// launch).
-bool decode_shared_in_gate_up() {
-  const char* env = getenv("MOE_DECODE_SHARED");
-  return !(env && env[0] == 'r');
 }
 
 size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
@@ -421,9 +404,39 @@ int run_down(const void* act, int T, int H, int E, int k, int I, const void* dow
 
 }  // namespace
 
+namespace moe {
+namespace {
+const char* const kKnobNames[kKnobCount] = {"MOE_DECODE",       "MOE_DECODE_DOWN",
+                                            "MOE_DECODE_GU_BLOCKS", "MOE_MIXED",
+                                            "MOE_PREFILL_SIDE", "MOE_PREFILL_SHARED_FIRST"};
+std::mutex g_knob_mu;
+std::atomic<bool> g_knobs_read{false};
+char g_knob_val[kKnobCount][32];
+bool g_knob_set[kKnobCount];
+
+void read_knobs() {
+  std::lock_guard<std::mutex> lock(g_knob_mu);
+  for (int i = 0; i < kKnobCount; ++i) {
+    const char* v = getenv(kKnobNames[i]);
+    g_knob_set[i] = v != nullptr;
+    snprintf(g_knob_val[i], sizeof g_knob_val[i], "%s", v ? v : "");
+  }
+  g_knobs_read.store(true, std::memory_order_release);
+}
+}  // namespace
+
+const char* knob(Knob k) {
+  if (!g_knobs_read.load(std::memory_order_acquire)) read_knobs();
+  return g_knob_set[k] ? g_knob_val[k] : nullptr;
+}
+}  // namespace moe
+
 extern "C" {
 
 int moe_abi_version(void) { return MOE_ABI_VERSION; }
+
+
+void moe_reload_tuning(void) { read_knobs(); }
 
 const char* moe_last_error(void) { return g_err.c_str(); }
 
@@ -831,7 +844,7 @@ int block_forward(const void* x, int T, int H, int E, int k, int I, int IS, cons
     d.sh_gate = static_cast<const uint16_t*>(sh_gate);
     d.sh_up = static_cast<const uint16_t*>(sh_up);
     d.sh_down = static_cast<const uint16_t*>(sh_down);
-    d.sh_in_gate_up = decode_shared_in_gate_up();
+    d.sh_in_gate_up = true;
     d.residual = static_cast<const uint16_t*>(residual);
     d.round_w = mode == MOE_ROUND_PRODUCT;
     d.logits = lg;
@@ -862,7 +875,7 @@ int block_forward(const void* x, int T, int H, int E, int k, int I, int IS, cons
   // The shared expert depends on x alone: where its projections would run as launches of
   // their own anyway (fp8 routed experts, prefill tiles), they run on the auxiliary stream
   // from the start of the block, beside the router and routing, and join before the combine.
-  AuxStream* aux = block_side_enabled(T, wdtype == MOE_WEIGHTS_FP8_E4M3, w.bm) ? aux_stream(s)
+  AuxStream* aux = block_side_enabled(wdtype == MOE_WEIGHTS_FP8_E4M3, w.bm) ? aux_stream(s)
                                                                                : nullptr;
   const int part = aux ? kRoutedOnly : kBoth;
   Fork fork(aux, s);  // joined before the combine, or on any early return

@@ -337,7 +337,7 @@ hipError_t launch_prefill_gemm(int mode, const GemmArgs& a_in, int max_tiles, hi
   a.MTgrid = max_tiles;
   a.shared_first = 0;
   if (a.table && a.op[0].N > 0 && a.op[1].N > 0) {
-    const char* env = getenv("MOE_PREFILL_SHARED_FIRST");
+    const char* env = knob(kKnobPrefillSharedFirst);
     if (!(env && env[0] == '0')) a.shared_first = (a.T + PBM - 1) / PBM;
   }
   const long long grid = (long long)((max_tiles + kXcds - 1) / kXcds) * kXcds * a.nrb;

@@ -17,14 +17,12 @@
 //   from global memory into registers in the MFMA operand layout (lane l: row l % 16,
 //   k = 8 (l / 16) .. + 8; 64 contiguous bytes of each of 16 rows per load instruction), R
 //   k-steps in flight per wave; LDS holds only the final reduction.
-// * k_router_tiles (prefill-sized batches): 64 tokens x 64 rows per workgroup, both operands
-//   staged through LDS and shared by 4 waves (2 x 2 blocks of 16 each); each wave runs the
-//   whole K, restarting its accumulator at every quarter and folding it into a running
-//   total, which reproduces ((s0 + s1) + s2) + s3 bit for bit with a quarter of the operand
-//   traffic of the split kernel.
-// * k_router_dma: the same tiles and order with the operands staged by global -> LDS DMA
-//   (the default from 768 tokens: 16.1 against 20.7 µs at 4096 tokens, 12.7 against 14.8
-//   at 768; k_router_tiles remains for MOE_ROUTER_DMA=0).
+// * k_router_dma (from 768 tokens): 64 tokens x 64 rows per workgroup, both operands staged
+//   by global -> LDS DMA and shared by 4 waves; each wave runs the whole K, restarting its
+//   accumulator at every quarter and folding it into a running total, which reproduces
+//   ((s0 + s1) + s2) + s3 bit for bit with a quarter of the operand traffic of the split
+//   kernel (16.1 against 20.7 µs for a register-staged form of the same tiles at 4096
+//   tokens, 12.7 against 14.8 at 768).
 // Workgroups of one token tile get ids 8 apart so they run on one XCD and share the tile's
 // token rows in its L2 (the router rows, 1.25 MiB, stay in every XCD's L2).
 #include <stdio.h>
@@ -161,118 +159,15 @@ constexpr int kTT = 64;                 // tokens per tile
 constexpr int kTN = 64;                 // router rows per tile
 constexpr int kTRows = kTT + kTN;       // staged rows per chunk (tokens, then router rows)
 
-// KC: k per staged chunk (KC / 8 16-byte units of each row; one barrier per chunk).
-template <int KC>
-__global__ __launch_bounds__(256) void k_router_tiles(RouterArgs a) {
-  constexpr int kTK = KC;
-  constexpr int kTUnits = kTK / 8;
-  constexpr int kTStageU4 = kTRows * kTUnits;  // one stage in uint4
-  constexpr int kTLoads = kTStageU4 / 256;     // 16-byte loads per thread per chunk
-  __shared__ uint4 lds[2 * kTStageU4];
-  int tile, rg;
-  if (a.xcd_map) {
-    const int xcd = blockIdx.x & (kXcdsR - 1);
-    const int j = blockIdx.x / kXcdsR;
-    tile = (j / a.nrg) * kXcdsR + xcd;
-    rg = j - (j / a.nrg) * a.nrg;
-    if (tile >= a.ntiles) return;
-  } else {
-    tile = blockIdx.x / a.nrg;
-    rg = blockIdx.x - tile * a.nrg;
-  }
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int wt = wave & 1, wn = wave >> 1;  // token half, row half of the tile
-  const int lr = lane & 15, kq = lane >> 4;
-  const int t0 = tile * kTT, n0 = rg * kTN;
-
-  // staging: thread tid moves 16-byte unit (tid + 256 i) of the chunk: row = u / kTUnits
-  // (tokens 0..63, then router rows), physical unit u % kTUnits holding logical unit
-  // (u % kTUnits) ^ (row % kTUnits)
-  const uint16_t* src[kTLoads];
-  int dst[kTLoads];
-#pragma unroll
-  for (int i = 0; i < kTLoads; ++i) {
-    const int u = tid + 256 * i;
-    const int row = u / kTUnits, pu = u % kTUnits;
-    const int lu = pu ^ (row & (kTUnits - 1));
-    src[i] = row < kTT ? a.x + (long long)min(t0 + row, a.T - 1) * a.H + lu * 8
-                       : a.w + (long long)min(n0 + row - kTT, a.n_pack - 1) * a.H + lu * 8;
-    dst[i] = u;
-  }
-  uint4 stage[kTLoads];
-  auto load = [&](int d) __attribute__((always_inline)) {
-#pragma unroll
-    for (int i = 0; i < kTLoads; ++i) stage[i] = ld16(src[i] + d * kTK);
-  };
-  auto store = [&](int buf) __attribute__((always_inline)) {
-#pragma unroll
-    for (int i = 0; i < kTLoads; ++i) lds[buf * kTStageU4 + dst[i]] = stage[i];
-  };
-
-  f32x4_t acc[2][2], tot[2][2];  // [token block][row block]
-#pragma unroll
-  for (int b = 0; b < 2; ++b)
-#pragma unroll
-    for (int r = 0; r < 2; ++r) acc[b][r] = tot[b][r] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-
-  const int nd = a.H / kTK;                      // chunks
-  const int per_q = nd / kRouterSplit;           // chunks per K quarter
-  load(0);
-  store(0);
-  if (nd > 1) load(1);
-  for (int d = 0; d < nd; ++d) {
-    __syncthreads();  // chunk d staged; the other buffer free
-    if (d + 1 < nd) store((d + 1) & 1);
-    if (d + 2 < nd) load(d + 2);
-    const uint4* st = lds + (d & 1) * kTStageU4;
-#pragma unroll
-    for (int h = 0; h < kTK / 32; ++h) {
-      const int lu = (h * 4 + kq) ^ (lr & (kTUnits - 1));
-      uint4 fa[2], fb[2];
-#pragma unroll
-      for (int r = 0; r < 2; ++r) fa[r] = st[(kTT + wn * 32 + r * 16 + lr) * kTUnits + lu];
-#pragma unroll
-      for (int b = 0; b < 2; ++b) fb[b] = st[(wt * 32 + b * 16 + lr) * kTUnits + lu];
-#pragma unroll
-      for (int b = 0; b < 2; ++b)
-#pragma unroll
-        for (int r = 0; r < 2; ++r) acc[b][r] = mfma16x16x32(fa[r], fb[b], acc[b][r]);
-    }
-    if ((d + 1) % per_q == 0) {  // end of a K quarter: total = ((s0 + s1) + s2) + s3
-#pragma unroll
-      for (int b = 0; b < 2; ++b)
-#pragma unroll
-        for (int r = 0; r < 2; ++r) {
-          tot[b][r] = d + 1 == per_q ? acc[b][r] : tot[b][r] + acc[b][r];
-          acc[b][r] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-        }
-    }
-  }
-  // lane (q = kq, j = lr) holds rows 4q .. 4q + 3 of token column j of each block
-#pragma unroll
-  for (int b = 0; b < 2; ++b) {
-    const int t = t0 + wt * 32 + b * 16 + lr;
-    if (t >= a.T) continue;
-#pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int n = n0 + wn * 32 + r * 16 + 4 * kq;
-      if (n >= a.n_pack) continue;  // n_pack is a multiple of 16: n < n_pack covers n + 3
-      const f32x4_t v = tot[b][r];
-      *reinterpret_cast<uint2*>(a.out + (long long)t * a.n_pack + n) =
-          make_uint2(pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3]));
-    }
-  }
-}
-
-// The same tile and summation order with the chunks staged by global -> LDS DMA
-// (global_load_lds_dwordx4: no registers on the way, more bytes in flight per CU) in a ring
-// of S stages, chunk d + S - 1 requested while chunk d is multiplied. Wave w's DMA load i
+// k_router_dma: 64 tokens x 64 router rows per workgroup, both operands staged by global ->
+// LDS DMA (global_load_lds_dwordx4: no registers on the way) and shared by 4 waves (2 x 2
+// blocks of 16 each), in a ring of S stages, chunk d + S - 1 requested while chunk d is
+// multiplied. Each wave runs the whole K, restarting its accumulator at every quarter and
+// folding it into a running total, which reproduces ((s0 + s1) + s2) + s3 bit for bit. Wave w's DMA load i
 // fills the 4-row group w + 4 i of a stage (1 KiB: 4 rows x 256 bytes), lane l writing
 // physical unit l & 15 of row l >> 4 of the group with logical unit (l & 15) ^ (row & 15):
-// the layout k_router_tiles writes, so the fragment reads are the same. Fragments are read
-// by inline asm with explicit waits (lds_dma.h). Bit-identical to k_router_tiles.
+// the XOR order that keeps the fragment reads (16 rows, one logical unit) bank-conflict
+// free. Fragments are read by inline asm with explicit waits (lds_dma.h).
 template <int S>
 __global__ __launch_bounds__(256) void k_router_dma(RouterArgs a) {
   constexpr int KC = 128;                       // k per chunk: 256 bytes of each row
@@ -393,17 +288,10 @@ struct RCfg {
 // bits). Measured per call at H=2048, n_pack=320 (8 launches graph-replayed): T <= 128
 // (1,1,4) 6.1-6.2 µs; 256 (2,1,8) 9.3; 512 (2,2,4) 11.4; 1024 (4,2,4) 15.9 (the tiled
 // kernel, 128-k chunks: 14.7 from ~1k tokens; 20.5 at 4096 against 39.7 here).
-// MOE_ROUTER_CFG "tb,rb,r" overrides it (tuning knob).
 RCfg router_cfg(int T) {
-  const char* env = getenv("MOE_ROUTER_CFG");
-  RCfg c{};
-  if (env && sscanf(env, "%d,%d,%d", &c.tb, &c.rb, &c.r) == 3) return c;
   if (T <= 128) return {1, 1, 4};
   if (T <= 384) return {2, 1, 8};
-  if (T <= 768) return {2, 2, 4};
-  if (T <= 1536) return {4, 2, 4};
-  if (T <= 3072) return {4, 4, 4};
-  return {4, 4, 2};
+  return {2, 2, 4};
 }
 
 }  // namespace
@@ -421,11 +309,7 @@ hipError_t launch_router_gemm(const void* x, int T, int H, const void* w_pack, i
   a.T = T;
   a.H = H;
   a.n_pack = n_pack;
-  const char* env_tiles = getenv("MOE_ROUTER_TILES");  // token count from which the tiles run
-  const int tiles_from = env_tiles ? atoi(env_tiles) : kRouterTilesFrom;
-  const char* env_kc = getenv("MOE_ROUTER_TILE_K");
-  const int kc = env_kc && atoi(env_kc) == 64 ? 64 : 128;
-  if (T >= tiles_from && H % (kRouterSplit * kc) == 0) {
+  if (T >= kRouterTilesFrom && H % (kRouterSplit * 128) == 0) {
     a.ntiles = (T + kTT - 1) / kTT;
     a.nrg = (n_pack + kTN - 1) / kTN;
     a.xcd_map = a.ntiles >= kXcdsR;
@@ -433,36 +317,24 @@ hipError_t launch_router_gemm(const void* x, int T, int H, const void* w_pack, i
                                ? (long long)((a.ntiles + kXcdsR - 1) / kXcdsR) * kXcdsR * a.nrg
                                : (long long)a.ntiles * a.nrg;
     if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
-    const char* env_dma = getenv("MOE_ROUTER_DMA");  // stages of the DMA kernel; 0: off
-    const int stages = env_dma ? atoi(env_dma) : 2;
-    if (kc == 128 && (stages == 2 || stages == 3)) {
-      const int bytes = stages * kTRows * 256;
-      const void* fn = stages == 3 ? reinterpret_cast<const void*>(&k_router_dma<3>)
-                                   : reinterpret_cast<const void*>(&k_router_dma<2>);
-      static std::mutex mu;
-      static uint64_t done[2] = {0, 0};  // bit d: device d, per stage count
-      int dev = 0;
-      hipError_t err = hipGetDevice(&dev);
-      if (err != hipSuccess) return err;
-      if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
-      {
-        std::lock_guard<std::mutex> lock(mu);
-        if (!(done[stages - 2] >> dev & 1)) {
-          err = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
-          if (err != hipSuccess) return err;
-          done[stages - 2] |= uint64_t(1) << dev;
-        }
+    constexpr int kStages = 2;
+    const int bytes = kStages * kTRows * 256;
+    static std::mutex mu;
+    static uint64_t done = 0;  // bit d: the LDS limit is raised on device d
+    int dev = 0;
+    hipError_t err = hipGetDevice(&dev);
+    if (err != hipSuccess) return err;
+    if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+    {
+      std::lock_guard<std::mutex> lock(mu);
+      if (!(done >> dev & 1)) {
+        err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_router_dma<kStages>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+        if (err != hipSuccess) return err;
+        done |= uint64_t(1) << dev;
       }
-      if (stages == 3)
-        hipLaunchKernelGGL(k_router_dma<3>, dim3((unsigned)grid), dim3(256), bytes, st, a);
-      else
-        hipLaunchKernelGGL(k_router_dma<2>, dim3((unsigned)grid), dim3(256), bytes, st, a);
-      return hipGetLastError();
     }
-    if (kc == 64)
-      hipLaunchKernelGGL(k_router_tiles<64>, dim3((unsigned)grid), dim3(256), 0, st, a);
-    else
-      hipLaunchKernelGGL(k_router_tiles<128>, dim3((unsigned)grid), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(k_router_dma<kStages>, dim3((unsigned)grid), dim3(256), bytes, st, a);
     return hipGetLastError();
   }
   const RCfg c = router_cfg(T);
@@ -479,19 +351,9 @@ hipError_t launch_router_gemm(const void* x, int T, int H, const void* w_pack, i
     hipLaunchKernelGGL((k_router_gemm<TB, RB, RR>), dim3((unsigned)grid), block, 0, st, a); \
     return hipGetLastError();                                                            \
   }
-  RL(1, 1, 8)
   RL(1, 1, 4)
-  RL(1, 1, 16)
-  RL(1, 2, 8)
   RL(2, 1, 8)
-  RL(2, 2, 8)
   RL(2, 2, 4)
-  RL(4, 1, 8)
-  RL(1, 4, 8)
-  RL(4, 2, 4)
-  RL(2, 4, 4)
-  RL(4, 4, 4)
-  RL(4, 4, 2)
 #undef RL
   return hipErrorInvalidValue;
 }

@@ -44,3 +44,39 @@ def max_abs(a, b):
 def mean_rel(a, b):
     a, b = a.float().cpu(), b.float().cpu()
     return ((a - b).abs().mean() / b.abs().mean().clamp_min(1e-30)).item()
+
+
+class knobs:
+    """Run the body with the library's comparison switches (MOE_DECODE, MOE_MIXED, ...) set
+    as given (None: unset). The library reads them once per process and again on
+    moe_reload_tuning(), which this calls on entry and exit."""
+
+    def __init__(self, **env):
+        self.env = env
+
+    def _reload(self):
+        import __graft_entry__
+
+        __graft_entry__.load_package()._lib.load().moe_reload_tuning()
+
+    def __enter__(self):
+        import os
+
+        self.old = {k: os.environ.get(k) for k in self.env}
+        for k, v in self.env.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+        self._reload()
+        return self
+
+    def __exit__(self, *exc):
+        import os
+
+        for k, v in self.old.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+        self._reload()

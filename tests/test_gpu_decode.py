@@ -13,13 +13,12 @@ tiled path, so:
 
 from __future__ import annotations
 
-import os
 
 import pytest
 import torch
 
 from oracle import moe_oracle as orc
-from tests.helpers import BF16, max_abs, mean_rel, routing
+from tests.helpers import BF16, knobs, max_abs, mean_rel, routing
 
 pytestmark = pytest.mark.gpu
 
@@ -28,18 +27,9 @@ def _say(*a):
     print(*a, flush=True)
 
 
-class _tiled:
+def _tiled():
     """Run the body with the decode path switched off (MOE_DECODE=0)."""
-
-    def __enter__(self):
-        self.old = os.environ.get("MOE_DECODE")
-        os.environ["MOE_DECODE"] = "0"
-
-    def __exit__(self, *exc):
-        if self.old is None:
-            os.environ.pop("MOE_DECODE", None)
-        else:
-            os.environ["MOE_DECODE"] = self.old
+    return knobs(MOE_DECODE="0")
 
 
 def _weights(dev, seed, H=2048, E=256, I=512, IS=512):
@@ -198,15 +188,8 @@ def test_decode_one_token_down_kernels_agree(pkg, dev, layer, fp8):
     x = torch.randn(1, 2048, generator=g).to(BF16).to(dev)
     r = torch.randn(1, 2048, generator=g).to(BF16).to(dev)
     a = pkg.block.moe(x, mlp, 8, decode=True, residual=r)
-    old = os.environ.get("MOE_DECODE_DOWN")
-    os.environ["MOE_DECODE_DOWN"] = "rows"
-    try:
+    with knobs(MOE_DECODE_DOWN="rows"):
         b = pkg.block.moe(x, mlp, 8, decode=True, residual=r)
-    finally:
-        if old is None:
-            os.environ.pop("MOE_DECODE_DOWN", None)
-        else:
-            os.environ["MOE_DECODE_DOWN"] = old
     torch.cuda.synchronize()
     assert torch.equal(a, b)
 
@@ -226,16 +209,9 @@ def test_decode_gate_up_row_blocks_agree(pkg, dev, layer, T, routes):
     x = x.to(BF16).to(dev)
     r = torch.randn(T, 2048, generator=g).to(BF16).to(dev)
     got = {}
-    old = os.environ.get("MOE_DECODE_GU_BLOCKS")
-    try:
-        for blocks in ("4", "2", "1"):
-            os.environ["MOE_DECODE_GU_BLOCKS"] = blocks
+    for blocks in ("4", "2", "1"):
+        with knobs(MOE_DECODE_GU_BLOCKS=blocks):
             got[blocks] = pkg.block.moe(x, mlp, 8, decode=True, residual=r, return_routing=True)
-    finally:
-        if old is None:
-            os.environ.pop("MOE_DECODE_GU_BLOCKS", None)
-        else:
-            os.environ["MOE_DECODE_GU_BLOCKS"] = old
     torch.cuda.synchronize()
     distinct = int(torch.unique(got["1"][1]).numel())
     _say(f"decode gate_up row blocks T={T} {routes}: {distinct} distinct experts")

@@ -15,7 +15,7 @@ import pytest
 import torch
 
 from oracle import moe_oracle as orc
-from tests.helpers import BF16, max_abs, mean_rel
+from tests.helpers import BF16, knobs, max_abs, mean_rel
 
 pytestmark = pytest.mark.gpu
 
@@ -130,17 +130,55 @@ def test_fp8_mixed_launch_matches_side_branch(pkg, dev, T):
     mlp.experts.down_proj, mlp.experts.down_scale = q2, s2
     x = torch.randn(T, Hh, generator=torch.Generator().manual_seed(T)).to(BF16).to(dev)
     a, ia, wa, _ = pkg.block.moe(x, mlp, 8, return_routing=True)
-    old = os.environ.get("MOE_MIXED")
-    os.environ["MOE_MIXED"] = "0"
-    try:
+    with knobs(MOE_MIXED="0"):
         b, ib, wb, _ = pkg.block.moe(x, mlp, 8, return_routing=True)
-    finally:
-        if old is None:
-            os.environ.pop("MOE_MIXED", None)
-        else:
-            os.environ["MOE_MIXED"] = old
     torch.cuda.synchronize()
     assert torch.equal(ia, ib) and torch.equal(wa, wb)
     scale = max(1.0, b.float().abs().max().item())
     print(f"fp8 mixed vs side branch T={T}: max {max_abs(a, b):.3g}", flush=True)
     assert max_abs(a, b) <= 4e-3 * scale
+
+
+def test_fp8_stack_of_layers_t32(pkg, dev):
+    """C5 as a stack: four independent full-shape layers with fp8-e4m3 experts (each from
+    its own bf16 N(0, 0.02) masters) at 32 tokens, in the bench's mode (decode=True: bf16
+    routing-weight products), each layer's input plus its output the next layer's input (the
+residual stream of a decoder stack, so the inputs keep their scale). Every layer:
+    routing bit-exact on the GPU logits, values against the fp32 oracle on the dequantised
+    weights (max-abs 2e-2, mean-rel 6e-3) and on the bf16 masters (5e-2 / 6e-2), taken on
+    the input that layer received."""
+    import __graft_entry__
+
+    Hh, E, I, T = 2048, 256, 512, 32
+    x = torch.randn(T, Hh, generator=torch.Generator().manual_seed(4321)).to(BF16).to(dev)
+    for layer in range(4):
+        gen = torch.Generator(device=dev).manual_seed(500 + layer)
+
+        def rnd(*shape):
+            return (torch.randn(*shape, generator=gen, device=dev) * 0.02).to(BF16)
+
+        w = {"router": rnd(E, Hh), "gate_up": rnd(E, 2 * I, Hh), "down": rnd(E, Hh, I),
+             "sh_gate": rnd(I, Hh), "sh_up": rnd(I, Hh), "sh_down": rnd(Hh, I),
+             "sh_gate_w": rnd(1, Hh)}
+        mlp = __graft_entry__._mlp_from_weights(w, dev)
+        q, s = pkg.fp8.quantize_rows(w["gate_up"])
+        q2, s2 = pkg.fp8.quantize_rows(w["down"])
+        mlp.experts.gate_up_proj, mlp.experts.gate_up_scale = q, s
+        mlp.experts.down_proj, mlp.experts.down_scale = q2, s2
+        out, idx, wts, logits = pkg.block.moe(x, mlp, 8, decode=True, return_routing=True)
+        torch.cuda.synchronize()
+        lg = logits.cpu()[:, :E]
+        ref_w, ref_i = orc.route(lg, 8)
+        assert torch.equal(idx.cpu(), ref_i) and torch.equal(wts.cpu(), ref_w), layer
+        xc = x.cpu()
+        wq = dict(w, gate_up=q, down=q2, gate_up_scale=s, down_scale=s2)
+        f32_q = orc.block_fp32(xc, wq, ref_i, logits=lg)
+        f32_m = orc.block_fp32(xc, w, ref_i, logits=lg)
+        print(f"fp8 stack layer {layer}: {int(torch.unique(ref_i).numel())} experts; vs "
+              f"dequantised fp32 max {max_abs(out, f32_q):.3g} mean-rel {mean_rel(out, f32_q):.3g}; "
+              f"vs bf16 masters mean-rel {mean_rel(out, f32_m):.3g}", flush=True)
+        assert torch.isfinite(out.float()).all()
+        assert max_abs(out, f32_q) <= 2e-2 and mean_rel(out, f32_q) <= 6e-3, layer
+        assert max_abs(out, f32_m) <= 5e-2 and mean_rel(out, f32_m) <= 6e-2, layer
+        x = (x.float() + out.float()).to(BF16)
+        del w, mlp, q, s, q2, s2, wq

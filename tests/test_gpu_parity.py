@@ -12,7 +12,7 @@ import pytest
 import torch
 
 from oracle import moe_oracle as orc
-from tests.helpers import BF16, max_abs, mean_rel, router_rows, routing
+from tests.helpers import BF16, knobs, max_abs, mean_rel, router_rows, routing
 
 pytestmark = pytest.mark.gpu
 
@@ -485,24 +485,15 @@ def test_prefill_shared_tile_order_and_side_launch_agree(pkg, dev, full_layer, T
     _, idx, _ = pkg.ops.route(logits, 8, experts=256)
     sp = pkg.ops.sort_pairs(idx, 256, shared=True)
     runs = {}
-    saved = {k: os.environ.get(k) for k in ("MOE_PREFILL_SIDE", "MOE_PREFILL_SHARED_FIRST")}
-    try:
-        for name, env in (("first", {}), ("table", {"MOE_PREFILL_SHARED_FIRST": "0"}),
-                          ("side", {"MOE_PREFILL_SIDE": "1"})):
-            for k in saved:
-                os.environ.pop(k, None)
-            os.environ.update(env)
+    for name, env in (("first", {}), ("table", {"MOE_PREFILL_SHARED_FIRST": "0"}),
+                      ("side", {"MOE_PREFILL_SIDE": "1"})):
+        env = {"MOE_PREFILL_SIDE": None, "MOE_PREFILL_SHARED_FIRST": None, **env}
+        with knobs(**env):
             act, act_sh = pkg.ops.grouped_gate_up(x, 8, w["gate_up"], sp,
                                                   shared=(w["sh_gate"], w["sh_up"]))
             y, y_sh = pkg.ops.grouped_down(act, T, 8, w["down"], sp, shared=(w["sh_down"], act_sh))
             torch.cuda.synchronize()
             runs[name] = (act.clone(), act_sh.clone(), y.clone(), y_sh.clone())
-    finally:
-        for k, v in saved.items():
-            if v is None:
-                os.environ.pop(k, None)
-            else:
-                os.environ[k] = v
     for name in ("table", "side"):
         for a, b in zip(runs["first"], runs[name]):
             assert torch.equal(a, b), name

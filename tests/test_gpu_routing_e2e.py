@@ -145,16 +145,20 @@ def test_routing_from_x_matches_cpu_linear(pkg, dev, uniform_layer, zipf_layer, 
          f"{n_same} tokens with bit-equal logits")
 
 
-def test_c3_zipf_full_workload(pkg, dev, zipf_layer):
+@pytest.mark.parametrize("decode", [True, False])
+def test_c3_zipf_full_workload(pkg, dev, zipf_layer, decode):
     """The C3 workload as the bench builds it: 64 tokens x + mu v on the Zipf(1.1) router.
     Routing (indices, weights), counts, offsets, order and tile table bit-exact against the
-    oracle on the GPU logits; values against the fp32 oracle within the bf16 bar."""
+    oracle on the GPU logits; values against the fp32 oracle within the bf16 bar and against
+    the reference torch path of the same mode: decode=True (the bench's C3 mode and
+    FusedDecode._moe's: routing-weight products rounded to bf16) and decode=False (exact
+    fp32 products, the grouped path's)."""
     w, v = zipf_layer
     T = 64
     g = torch.Generator().manual_seed(77)
     x = (torch.randn(T, H, generator=g) + _synth().ZIPF_MU * v[None, :]).to(BF16)
     mlp = _gpu_mlp(w, dev)
-    out, idx, wts, logits = pkg.block.moe(x.to(dev), mlp, K, return_routing=True)
+    out, idx, wts, logits = pkg.block.moe(x.to(dev), mlp, K, decode=decode, return_routing=True)
     torch.cuda.synchronize()
     lg = logits.cpu()[:, :E]
     ref_w, ref_i = orc.route(lg, K)
@@ -177,9 +181,9 @@ def test_c3_zipf_full_workload(pkg, dev, zipf_layer):
     assert [(int(tab[t]), int(tab[mt + t]), int(tab[2 * mt + t])) for t in range(n)] == tiles
     f32 = orc.block_fp32(x, w, ref_i, logits=lg)
     wc, ic = orc.compact_experts(w, ref_i)
-    ref = orc.block_bf16_routed(x, wc, ic, wts.cpu(), logits.cpu()[:, E:E + 1], decode=True)
+    ref = orc.block_bf16_routed(x, wc, ic, wts.cpu(), logits.cpu()[:, E:E + 1], decode=decode)
     ours, theirs = mean_rel(out, f32), mean_rel(ref, f32)
-    _say(f"C3 vs fp32: max {max_abs(out, f32):.3g} mean-rel {ours:.3g}; reference path "
+    _say(f"C3 decode={decode} vs fp32: max {max_abs(out, f32):.3g} mean-rel {ours:.3g}; reference path "
          f"mean-rel {theirs:.3g}; ours vs reference path {max_abs(out, ref):.3g}")
     assert max_abs(out, f32) <= 2e-2 and max_abs(out, ref) <= 2e-2
     assert ours <= max(5e-3, 1.1 * theirs)

@@ -6,11 +6,13 @@ independent of the row count").
 Within one path (decode, tiled, prefill) the per-row arithmetic is fixed: the router's dot
 products, the top-k, each expert projection's K order and the combine are per token, so
 the comparison is bitwise. The router GEMM of the tiled and prefill paths sums every logit
-in one fixed order at every batch size (its small-batch and its tiled prefill kernels give
-the same bits: 1100 -> 900 and 2048 -> 100 cross from one to the other; 2048 -> 100 also
+in one fixed order at every batch size: its split kernel (below 768 tokens, in three tile
+configurations switching at 128 and 384 tokens) and its LDS-tiled DMA kernel (from 768)
+give the same bits. 800 -> 700, 1024 -> 600 and 2048 -> 100 cross from the DMA kernel to
+the split one (1024 -> 600 and 800 -> 700 within the prefill GEMM tiles; 2048 -> 100 also
 crosses from the prefill GEMM tiles to the tiled expert GEMM, so there only the routing is
-bitwise), so the logits
-themselves are bitwise too. Across
+bitwise), 512 -> 300 and 300 -> 129 between split configurations. So the logits themselves
+are bitwise too. Across
 paths the fp32 summation order of a projection differs and only the bf16 tolerance applies
 (tested elsewhere)."""
 
@@ -38,6 +40,7 @@ def mlp(dev):
                                               (255, 17, False), (512, 300, False), (300, 129, False),
                                               (1536, 1024, False),
                                               (4096, 2048, False), (1100, 900, False),
+                                              (800, 700, False), (1024, 600, False),
                                               (2048, 100, False)])
 def test_leading_rows_match_smaller_batch(pkg, dev, mlp, big, small, decode):
     print(f"row independence {big} -> {small} decode={decode}", flush=True)
