@@ -480,6 +480,76 @@ def pmc_summary(fetch_dir, write_dir, copy_mib, config):
     print(md.read_text())
 
 
+def trace_summary(trace_dir, config):
+    """Per-layer timeline of the timed graph replay from a `rocprofv3 --kernel-trace` run of
+    `bench.py --configs <config> --no-cpu`: the library's dispatches sorted by start, split
+    where the device idles more than 50 us, the longest such run kept (the timed replay);
+    its period is where the first kernel name recurs. Per position of the period: median
+    start offset from the layer's first kernel, duration, and the gap since the previous
+    dispatch ended. Written to profiles/timeline_<config>.md."""
+    import csv
+    import statistics
+
+    paths = sorted(Path(trace_dir).rglob("*kernel_trace.csv"))
+    if not paths:
+        raise SystemExit(f"no kernel_trace.csv under {trace_dir}")
+    rows = []
+    for path in paths:
+        with open(path) as f:
+            for r in csv.DictReader(f):
+                if "moe::" in r["Kernel_Name"]:
+                    name = (r["Kernel_Name"].replace("void ", "")
+                            .replace("(anonymous namespace)::", "").split("(")[0])
+                    rows.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), name))
+    rows.sort()
+    runs, cur = [], [rows[0]]
+    for r in rows[1:]:
+        if r[0] - max(c[1] for c in cur[-4:]) > 200_000:
+            runs.append(cur)
+            cur = []
+        cur.append(r)
+    runs.append(cur)
+    run = max(runs, key=len)
+    # the period starts at the router launch (the first kernel of a layer)
+    start = next((i for i, r in enumerate(run) if "router" in r[2]), 0)
+    run = run[start:]
+    first = run[0][2]
+    period = next((i for i in range(1, len(run)) if run[i][2] == first), len(run))
+    layers = [run[i:i + period] for i in range(0, len(run) - period + 1, period)
+              if [r[2] for r in run[i:i + period]] == [r[2] for r in run[:period]]]
+    layers = layers[1:-1] if len(layers) > 4 else layers  # drop the replay's ramp and tail
+    starts = [ly[0][0] for ly in layers]
+    per = statistics.median(b - a for a, b in zip(starts, starts[1:])) / 1e3 if len(starts) > 1 else 0
+    lines = [f"# Timeline of one {config} layer in the timed graph replay\n",
+             "Commands (from the repository root on one MI355X; `cd /tmp && export TMPDIR=/tmp` "
+             "first, paths absolute):\n",
+             f"    rocprofv3 --kernel-trace --output-format csv -d <out> -o run -- python3 bench.py "
+             f"--configs {config} --no-cpu",
+             f"    python3 bench.py --trace-summary <out> --trace-config {config}\n",
+             f"{len(layers)} layers of the longest back-to-back run of library dispatches "
+             f"({len(run)} dispatches); medians in microseconds. Layer period (first kernel "
+             f"start to the next layer's first kernel start): **{per:.2f} us**.\n",
+             "| # | kernel | start offset | duration | gap before (since previous dispatch ended) |",
+             "|---|---|---|---|---|"]
+    busy = 0.0
+    for i in range(period):
+        off = statistics.median((ly[i][0] - ly[0][0]) / 1e3 for ly in layers)
+        dur = statistics.median((ly[i][1] - ly[i][0]) / 1e3 for ly in layers)
+        if i:
+            gap = statistics.median((ly[i][0] - ly[i - 1][1]) / 1e3 for ly in layers)
+        else:
+            gap = statistics.median((layers[j][0][0] - layers[j - 1][-1][1]) / 1e3
+                                    for j in range(1, len(layers))) if len(layers) > 1 else 0.0
+        busy += dur
+        lines.append(f"| {i} | `{layers[0][i][2]}` | {off:.2f} | {dur:.2f} | {gap:.2f} |")
+    lines.append(f"\nSum of the medians of the kernel durations: {busy:.2f} us of the {per:.2f} us "
+                 f"period; the rest ({per - busy:.2f} us) is time between dispatches. A negative "
+                 "gap is an overlap (the next dispatch started before the previous ended).")
+    md = ROOT / "profiles" / f"timeline_{config}.md"
+    md.write_text("\n".join(lines) + "\n")
+    print(md.read_text())
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -497,7 +567,14 @@ def main():
                          "`bench.py --calibrate-copy M --configs c` into profiles/ and exit")
     ap.add_argument("--pmc-copy-mib", type=int, default=256)
     ap.add_argument("--pmc-config", default="c2")
+    ap.add_argument("--trace-summary", metavar="TRACE_DIR",
+                    help="summarise a rocprofv3 --kernel-trace run of `bench.py --configs c` "
+                         "into profiles/timeline_<c>.md and exit")
+    ap.add_argument("--trace-config", default="c2")
     args = ap.parse_args()
+    if args.trace_summary:
+        trace_summary(args.trace_summary, args.trace_config)
+        return
     if args.pmc_summary:
         pmc_summary(args.pmc_summary[0], args.pmc_summary[1], args.pmc_copy_mib, args.pmc_config)
         return

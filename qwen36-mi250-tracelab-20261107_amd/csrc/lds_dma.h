@@ -34,13 +34,14 @@ __device__ __forceinline__ f32x4_t mfma_frag(u32x4v a, u32x4v b, f32x4_t c) {
                                                  __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
 }
 
-// Wait until at most n (0..12) of this wave's DMA loads are still in flight.
+// Wait until at most n (0..24) of this wave's DMA loads are still in flight.
 __device__ __forceinline__ void wait_loads(int n) {
   switch (n) {
 #define W(N)                                              \
   case N:                                                 \
     asm volatile("s_waitcnt vmcnt(" #N ")" ::: "memory"); \
     break;
+    W(24) W(23) W(22) W(21) W(20) W(19) W(18) W(17) W(16) W(15) W(14) W(13)
     W(12) W(11) W(10) W(9) W(8) W(7) W(6) W(5) W(4) W(3) W(2) W(1)
 #undef W
     default:

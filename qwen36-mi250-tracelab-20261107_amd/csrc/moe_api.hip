@@ -27,6 +27,12 @@ hipError_t launch_route_sort(const uint16_t* logits, long long ld, const int* id
 size_t sort_scratch_bytes(int P, int E);
 bool sort_uses_small(int P, int E);
 bool router_gemm_fits(int H, int n_pack);
+bool router_part_takes(int T, int H, int n_pack);
+hipError_t launch_router_part(const void* x, int T, int H, const void* w_pack, int n_pack,
+                              float* part, hipStream_t st);
+hipError_t launch_route_part(const float* part, int T, int n_pack, int E, int k,
+                             uint16_t* logits, long long* idx64, int* idx32, uint16_t* w_out,
+                             hipStream_t s);
 hipError_t launch_router_gemm(const void* x, int T, int H, const void* w_pack, int n_pack,
                               void* logits, hipStream_t st);
 hipError_t launch_combine(const uint16_t* y, const uint16_t* w, int k, const uint16_t* ysh,
@@ -763,6 +769,7 @@ struct BlockWs {
   uint16_t* w;
   int *counts, *offsets, *order, *table, *scratch;
   uint16_t *act, *act_sh, *y, *y_sh;
+  float* part;  // the router's fp32 K-quarter partial sums (router_part_takes)
   size_t bytes;
   int MT, bm;
 };
@@ -786,6 +793,7 @@ BlockWs carve_block(void* base, int T, int H, int E, int k, int I, int IS, int n
   w.act_sh = c.take<uint16_t>((size_t)T * IS);
   w.y = c.take<uint16_t>((size_t)P * H);
   w.y_sh = c.take<uint16_t>((size_t)T * H);
+  w.part = router_part_takes(T, H, n_pack) ? c.take<float>(4 * (size_t)T * n_pack) : nullptr;
   w.bytes = c.off;
   return w;
 }
@@ -888,12 +896,22 @@ int block_forward(const void* x, int T, int H, int E, int k, int I, int IS, cons
                   w.table, w.MT, w.bm, w.y, w.y_sh, fork.aux(), kSharedOnly);
     if (rc) return rc;
   }
-  rc = moe_router_logits(x, T, H, w_pack, n_pack, lg, stream);
-  if (rc) return rc;
-  HIP_TRY(launch_route_sort(lg, n_pack, nullptr, nullptr, T, E, k, w.bm, aux ? 0 : 1, i64,
-                            w.idx32, wt, w.counts, w.offsets, w.order, w.table, w.MT, w.scratch,
-                            s),
-          "route/sort launch");
+  if (w.part) {
+    // router partial sums, then the routing (which writes the logits), then the sort
+    HIP_TRY(launch_router_part(x, T, H, w_pack, n_pack, w.part, s), "router launch");
+    HIP_TRY(launch_route_part(w.part, T, n_pack, E, k, lg, i64, w.idx32, wt, s), "route launch");
+    HIP_TRY(launch_route_sort(nullptr, 0, w.idx32, nullptr, T, E, k, w.bm, aux ? 0 : 1, nullptr,
+                              nullptr, nullptr, w.counts, w.offsets, w.order, w.table, w.MT,
+                              w.scratch, s),
+            "sort launch");
+  } else {
+    rc = moe_router_logits(x, T, H, w_pack, n_pack, lg, stream);
+    if (rc) return rc;
+    HIP_TRY(launch_route_sort(lg, n_pack, nullptr, nullptr, T, E, k, w.bm, aux ? 0 : 1, i64,
+                              w.idx32, wt, w.counts, w.offsets, w.order, w.table, w.MT,
+                              w.scratch, s),
+            "route/sort launch");
+  }
   rc = run_gate_up(x, T, H, E, k, I, gate_up, gu_scale, wdtype, sh_gate, sh_up, IS, w.order,
                    w.table, w.MT, w.bm, w.act, w.act_sh, s, part);
   if (rc) return rc;

@@ -33,6 +33,44 @@ __global__ __launch_bounds__(256) void k_route(const uint16_t* __restrict__ logi
   route_rows<EPL>(logits, ld, t, E, k, lane, idx64, idx32, w_out, nullptr, counts);
 }
 
+// Routing from the router's four fp32 K-quarter partial sums (k_router_part): the logits
+// are bf16(((s0 + s1) + s2) + s3), the bits every router kernel gives; each token's row is
+// written to `logits` (all n_pack entries) and routed from registers.
+template <int EPL>
+__global__ __launch_bounds__(256) void k_route_part(const float* __restrict__ part, int T,
+                                                    int n_pack, int E, int k,
+                                                    uint16_t* __restrict__ logits,
+                                                    long long* __restrict__ idx64,
+                                                    int* __restrict__ idx32,
+                                                    uint16_t* __restrict__ w_out) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (t >= T) return;
+  const long long qs = (long long)T * n_pack;  // stride between quarters
+  const float* p = part + (long long)t * n_pack;
+  uint16_t* lrow = logits + (long long)t * n_pack;
+  auto logit = [&](int e) __attribute__((always_inline)) {
+    return f2bf_bits(((p[e] + p[qs + e]) + p[2 * qs + e]) + p[3 * qs + e]);
+  };
+  uint16_t raw[EPL];
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) {
+    const int e = lane + kWave * i;
+    raw[i] = e < n_pack ? logit(e) : 0;
+    if (e < n_pack) lrow[e] = raw[i];
+  }
+  for (int e = kWave * EPL + lane; e < n_pack; e += kWave) lrow[e] = logit(e);
+  int my_i;
+  float my_w;
+  route_row_raw<EPL>(raw, E, k, lane, my_i, my_w);
+  if (lane < k) {
+    const long long pidx = (long long)t * k + lane;
+    if (idx64) idx64[pidx] = my_i;
+    if (idx32) idx32[pidx] = my_i;
+    if (w_out) w_out[pidx] = f2bf_bits(my_w);
+  }
+}
+
 // ------------------------------------------------------------------- small fused path
 
 template <int EPL>
@@ -157,6 +195,17 @@ hipError_t launch_route(const uint16_t* logits, long long ld, int T, int E, int 
   if (T <= 0) return hipSuccess;
   dim3 grid((T + 3) / 4), block(256);
 #define L(EPL) hipLaunchKernelGGL(k_route<EPL>, grid, block, 0, s, logits, ld, T, E, k, idx64, idx32, w_out, counts)
+  MOE_EPL_DISPATCH(E, L);
+#undef L
+  return hipGetLastError();
+}
+
+hipError_t launch_route_part(const float* part, int T, int n_pack, int E, int k,
+                             uint16_t* logits, long long* idx64, int* idx32, uint16_t* w_out,
+                             hipStream_t s) {
+  if (T <= 0) return hipSuccess;
+  dim3 grid((T + 3) / 4), block(256);
+#define L(EPL) hipLaunchKernelGGL(k_route_part<EPL>, grid, block, 0, s, part, T, n_pack, E, k, logits, idx64, idx32, w_out)
   MOE_EPL_DISPATCH(E, L);
 #undef L
   return hipGetLastError();

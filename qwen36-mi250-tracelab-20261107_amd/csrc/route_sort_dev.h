@@ -169,11 +169,8 @@ __device__ __forceinline__ uint32_t bf16_from_order_key(uint32_t k) {
 // Order keys of one row's logits (lane l holds entries l + 64 i, i < EPL), sorted
 // descending per lane: key = (order key of the bf16 logit) << 16 | (0xffff - expert).
 template <int EPL>
-__device__ __forceinline__ void route_keys(const uint16_t* __restrict__ lrow, int E, int lane,
-                                           uint16_t (&raw)[EPL], uint32_t (&key)[EPL]) {
-  // all EPL loads in flight at once (clamped addresses, masked after)
-#pragma unroll
-  for (int i = 0; i < EPL; ++i) raw[i] = lrow[min(lane + kWave * i, E - 1)];
+__device__ __forceinline__ void route_keys_raw(const uint16_t (&raw)[EPL], int E, int lane,
+                                               uint32_t (&key)[EPL]) {
 #pragma unroll
   for (int i = 0; i < EPL; ++i) {
     int e = lane + kWave * i;
@@ -187,6 +184,14 @@ __device__ __forceinline__ void route_keys(const uint16_t* __restrict__ lrow, in
       key[i - 1] = hi;
       key[i] = lo;
     }
+}
+template <int EPL>
+__device__ __forceinline__ void route_keys(const uint16_t* __restrict__ lrow, int E, int lane,
+                                           uint16_t (&raw)[EPL], uint32_t (&key)[EPL]) {
+  // all EPL loads in flight at once (clamped addresses, masked after)
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) raw[i] = lrow[min(lane + kWave * i, E - 1)];
+  route_keys_raw<EPL>(raw, E, lane, key);
 }
 
 // One selection round: the previous round's winner (the lane whose head key is m; keys
@@ -242,6 +247,24 @@ __device__ void route_finish(const uint16_t (&raw)[EPL], uint32_t top, uint32_t 
   }
   my_idx = mine_i;
   my_w = mine_p / tot;
+}
+
+// route_row on logits already in registers (lane l: entries l + 64 i; raw is read only for
+// entries below E).
+template <int EPL>
+__device__ void route_row_raw(const uint16_t (&raw)[EPL], int E, int k, int lane, int& my_idx,
+                              float& my_w) {
+  uint32_t key[EPL];
+  route_keys_raw<EPL>(raw, E, lane, key);
+  const int rounds = min(k + 1, E);
+  uint32_t m = wave_max_u32(key[0]);
+  const uint32_t top = m;
+  uint32_t sel = lane == 0 ? m : 0u;
+  for (int j = 1; j < rounds; ++j) {
+    m = route_next<EPL>(key, m);
+    sel = lane == j ? m : sel;
+  }
+  route_finish<EPL>(raw, top, sel, rounds, E, k, lane, my_idx, my_w);
 }
 
 template <int EPL>

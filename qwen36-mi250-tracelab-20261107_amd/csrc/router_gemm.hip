@@ -153,6 +153,47 @@ __global__ __launch_bounds__(64 * kRouterSplit) void k_router_gemm(RouterArgs a)
   }
 }
 
+// k_router_part: the split kernel's work with one wave per workgroup, i.e. one K quarter
+// of one 16-token x 16-row block per workgroup (four times as many workgroups, each a
+// quarter of the chain), its fp32 partial sum stored to part[q][t][n]. The caller sums the
+// quarters as ((s0 + s1) + s2) + s3 and rounds (k_route_part), which gives the same logits
+// as k_router_gemm. For small batches, where k_router_gemm has too few workgroups to fill
+// the GPU.
+template <int NST>
+__global__ __launch_bounds__(64) void k_router_part(RouterArgs a, float* __restrict__ part) {
+  // the four quarter workgroups of a block get ids 8 apart: one XCD fetches the block's rows
+  // whole (as the four waves of a k_router_gemm workgroup do)
+  const int xcd = blockIdx.x & (kXcdsR - 1);
+  const int i = blockIdx.x / kXcdsR;
+  const int wk = i & (kRouterSplit - 1);
+  const int blk = (i / kRouterSplit) * kXcdsR + xcd;
+  if (blk >= a.ntiles * a.nrg) return;
+  const int tile = blk / a.nrg;
+  const int rg = blk - tile * a.nrg;
+  const int lane = threadIdx.x;
+  const int lr = lane & 15;
+  const int q = lane >> 4;
+  const int kbeg = wk * NST * 32;  // the quarter: NST k-steps of 32
+  const int t0 = tile * 16;
+  const int n0 = rg * 16;
+  const uint16_t* wa = a.w + (long long)(n0 + lr) * a.H + kbeg + q * 8;
+  const uint16_t* xb = a.x + (long long)min(t0 + lr, a.T - 1) * a.H + kbeg + q * 8;
+  // the whole quarter's operands in flight at once
+  uint4 ra[NST], rx[NST];
+#pragma unroll
+  for (int s = 0; s < NST; ++s) {
+    ra[s] = ld16(wa + s * 32);
+    rx[s] = ld16(xb + s * 32);
+  }
+  f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < NST; ++s) acc = mfma16x16x32(ra[s], rx[s], acc);
+  // lane (q, j = lr) holds rows 4q .. 4q + 3 of token column j
+  const int t = t0 + lr;
+  if (t < a.T)
+    *reinterpret_cast<f32x4_t*>(part + ((long long)wk * a.T + t) * a.n_pack + n0 + 4 * q) = acc;
+}
+
 // ------------------------------------------------------------------ LDS-tiled form
 
 constexpr int kTT = 64;                 // tokens per tile
@@ -297,6 +338,49 @@ RCfg router_cfg(int T) {
 }  // namespace
 
 bool router_gemm_fits(int H, int n_pack) { return H % (32 * kRouterSplit) == 0 && n_pack % 16 == 0; }
+
+// The block forward's router for T tokens: k_router_part + k_route_part where the routing is
+// a launch of its own anyway (more than 16 tokens) and the split kernel has few workgroups.
+// Measured per layer (8 layers cycled, uniform routing): 17 / 32 / 64 / 128 / 256 tokens
+// 154.0 / 207.8 / 263.9 / 297.8 / 318.9 µs against 155.4 / 209.8 / 265.6 / 298.8 / 320.6
+// with k_router_gemm then k_route; level at 512 tokens (372.8 against 371.9), slower at 767
+// (390.1 against 386.2). At C3 the router launch takes 4.8 µs against 7.7.
+bool router_part_takes(int T, int H, int n_pack) {
+  const int nst = H / (32 * kRouterSplit);
+  return router_gemm_fits(H, n_pack) && (nst == 4 || nst == 8 || nst == 16) && T > 16 &&
+         T <= 256;
+}
+
+hipError_t launch_router_part(const void* x, int T, int H, const void* w_pack, int n_pack,
+                              float* part, hipStream_t st) {
+  if (!router_gemm_fits(H, n_pack)) return hipErrorInvalidValue;
+  if (T <= 0) return hipSuccess;
+  RouterArgs a{};
+  a.x = static_cast<const uint16_t*>(x);
+  a.w = static_cast<const uint16_t*>(w_pack);
+  a.T = T;
+  a.H = H;
+  a.n_pack = n_pack;
+  a.ntiles = (T + 15) / 16;
+  a.nrg = n_pack / 16;
+  const long long nblk = (long long)a.ntiles * a.nrg;
+  const long long grid = (nblk + kXcdsR - 1) / kXcdsR * kXcdsR * kRouterSplit;
+  if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
+  switch (H / (32 * kRouterSplit)) {
+    case 4:
+      hipLaunchKernelGGL(k_router_part<4>, dim3((unsigned)grid), dim3(64), 0, st, a, part);
+      break;
+    case 8:
+      hipLaunchKernelGGL(k_router_part<8>, dim3((unsigned)grid), dim3(64), 0, st, a, part);
+      break;
+    case 16:
+      hipLaunchKernelGGL(k_router_part<16>, dim3((unsigned)grid), dim3(64), 0, st, a, part);
+      break;
+    default:
+      return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
 
 hipError_t launch_router_gemm(const void* x, int T, int H, const void* w_pack, int n_pack,
                               void* logits, hipStream_t st) {
