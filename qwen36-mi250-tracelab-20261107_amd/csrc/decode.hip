@@ -34,6 +34,7 @@
 #include "moe_common.h"
 #include "route_sort_dev.h"
 #include "add_rms.h"
+#include "lds_dma.h"
 #include "decode.h"
 
 namespace moe {
@@ -415,16 +416,16 @@ __attribute__((amdgpu_waves_per_eu(HC <= 4 ? 4 : 1))) void k_dec_gate_up_multi(D
   const int slot = bid / ngrp;
   const int blk0 = (bid - slot * ngrp) * G;  // first row block of this workgroup
 
-  // token rows into registers now (independent of the routing), into LDS after it
+  // token rows straight into LDS by DMA (no registers: the loads stay in flight through the
+  // routing below and are waited for at the barrier after it)
   constexpr int kXUnits = NT * kRowU4;
-  constexpr int kXPer = (kXUnits + 64 * kGuWaves - 1) / (64 * kGuWaves);  // per thread
-  uint4 xs[kXPer];
+  static_assert(kXUnits % (64 * kGuWaves) == 0, "whole waves of 16-byte units");
 #pragma unroll
-  for (int i = 0; i < kXPer; ++i) {
+  for (int i = 0; i < kXUnits / (64 * kGuWaves); ++i) {
     const int u = threadIdx.x + i * 64 * kGuWaves;
     const int t = u / kRowU4;
-    if (u < kXUnits)
-      xs[i] = reinterpret_cast<const uint4*>(a.x + (long long)min(t, a.T - 1) * H)[u - t * kRowU4];
+    dma16(reinterpret_cast<const uint4*>(a.x + (long long)min(t, a.T - 1) * H) + (u - t * kRowU4),
+          &s_x[i * 64 * kGuWaves + wave * 64]);
   }
 
   // routing: wave t routes token t; key of lane p = the expert of pair p (lanes < P)
@@ -449,9 +450,7 @@ __attribute__((amdgpu_waves_per_eu(HC <= 4 ? 4 : 1))) void k_dec_gate_up_multi(D
     s_idx[threadIdx.x] = ev;
     if (bid == 0) a.idx32[threadIdx.x] = ev;
   }
-#pragma unroll
-  for (int i = 0; i < kXPer; ++i)
-    if (threadIdx.x + i * 64 * kGuWaves < kXUnits) s_x[threadIdx.x + i * 64 * kGuWaves] = xs[i];
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's token-row DMA loads have landed
   __syncthreads();
   const int key = lane < P ? s_idx[lane] : -1;
   // distinct experts numbered in first-use order (pair order)

@@ -49,6 +49,13 @@ __device__ __forceinline__ void wait_loads(int n) {
   }
 }
 
+// One global -> LDS DMA load of a wave: lane l's 16 bytes at g go to lds + 16 l (lds is
+// wave-uniform). A plain function, so that the builtin's operands are checked once and not
+// per template instantiation of its callers (where the host pass would drop the kernel).
+__device__ __forceinline__ void dma16(const void* g, void* lds) {
+  __builtin_amdgcn_global_load_lds(g, lds, 16, 0, 0);
+}
+
 // The LDS byte address of a __shared__ / dynamic-shared pointer.
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   typedef __attribute__((address_space(3))) const char lds_char;
