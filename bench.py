@@ -480,6 +480,72 @@ def pmc_summary(fetch_dir, write_dir, copy_mib, config):
     print(md.read_text())
 
 
+def counter_summary(dirs, config, name, commands):
+    """Per-kernel medians of the SQ counters in one or more `rocprofv3 --pmc` runs (one
+    counter set per run) of `bench.py --configs <config>`, for the launches of each kernel
+    with its largest grid (the block's routed launches; the shared expert's side launches
+    of the same kernel have smaller grids), with the ratios read from them. Written to
+    profiles/<name>.md."""
+    import csv
+    import glob
+    import statistics
+
+    vals = {}   # kernel -> counter -> [values]
+    grids = {}  # kernel -> max grid
+    rows = []
+    for d in dirs:
+        for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            for r in csv.DictReader(open(f)):
+                if "moe::" not in r["Kernel_Name"]:
+                    continue
+                k = (r["Kernel_Name"].replace("void ", "").replace("(anonymous namespace)::", "")
+                     .split("(")[0])
+                g = int(r["Grid_Size"])
+                rows.append((k, g, r["Counter_Name"], float(r["Counter_Value"])))
+                grids[k] = max(grids.get(k, 0), g)
+    for k, g, c, v in rows:
+        if g == grids[k]:
+            vals.setdefault(k, {}).setdefault(c, []).append(v)
+    counters = sorted({c for kv in vals.values() for c in kv})
+    kernels = sorted(vals, key=lambda k: -max(statistics.median(v) for v in vals[k].values()))
+    med = {k: {c: statistics.median(vals[k][c]) for c in vals[k]} for k in kernels}
+    lines = [f"# SQ counters of the {config} kernels\n",
+             "Commands (from the repository root on one MI355X; `cd /tmp && export TMPDIR=/tmp` "
+             "first, paths absolute; one counter set per run):\n"]
+    lines += ["    " + c for c in commands]
+    lines += [f"    python3 bench.py --counter-summary <dir> [<dir> ...] --counter-config {config} "
+              f"--counter-name {name}\n",
+              "Medians per dispatch over the launches of each kernel with its largest grid, as "
+              "rocprofv3 reports them.\n",
+              "| counter | " + " | ".join(f"`{k}`" for k in kernels) + " |",
+              "|---|" + "---|" * len(kernels)]
+    for c in counters:
+        lines.append(f"| `{c}` | " + " | ".join(
+            f"{med[k][c]:.4g}" if c in med[k] else "" for k in kernels) + " |")
+
+    def ratio(k, a, b):
+        m = med[k]
+        return f"{m[a] / m[b]:.3f}" if a in m and b in m and m[b] else ""
+
+    derived = [("SQ_WAIT_ANY / SQ_WAVE_CYCLES (share of wave time in s_waitcnt)", "SQ_WAIT_ANY",
+                "SQ_WAVE_CYCLES"),
+               ("SQ_INSTS_VALU / SQ_INSTS_VMEM_RD (VALU instructions per load instruction)",
+                "SQ_INSTS_VALU", "SQ_INSTS_VMEM_RD"),
+               ("SQ_INST_LEVEL_VMEM / SQ_WAVE_CYCLES (load instructions in flight per wave)",
+                "SQ_INST_LEVEL_VMEM", "SQ_WAVE_CYCLES"),
+               ("SQ_VALU_MFMA_BUSY_CYCLES / SQ_BUSY_CYCLES", "SQ_VALU_MFMA_BUSY_CYCLES",
+                "SQ_BUSY_CYCLES")]
+    lines += ["", "| ratio | " + " | ".join(f"`{k}`" for k in kernels) + " |",
+              "|---|" + "---|" * len(kernels)]
+    for label, a, b in derived:
+        cells = [ratio(k, a, b) for k in kernels]
+        if any(cells):
+            lines.append(f"| {label} | " + " | ".join(cells) + " |")
+    md = ROOT / "profiles" / f"{name}.md"
+    md.write_text("\n".join(lines) + "\n")
+    print(md.read_text())
+
+
 def trace_summary(trace_dir, config):
     """Per-layer timeline of the timed graph replay from a `rocprofv3 --kernel-trace` run of
     `bench.py --configs <config> --no-cpu`: the library's dispatches sorted by start, split
@@ -571,7 +637,18 @@ def main():
                     help="summarise a rocprofv3 --kernel-trace run of `bench.py --configs c` "
                          "into profiles/timeline_<c>.md and exit")
     ap.add_argument("--trace-config", default="c2")
+    ap.add_argument("--counter-summary", nargs="+", metavar="PMC_DIR",
+                    help="summarise rocprofv3 --pmc runs of `bench.py --configs c` into "
+                         "profiles/<--counter-name>.md and exit")
+    ap.add_argument("--counter-config", default="c4")
+    ap.add_argument("--counter-name", default="counters")
+    ap.add_argument("--counter-commands", nargs="*", default=[],
+                    help="the rocprofv3 commands of the runs (quoted, for the summary)")
     args = ap.parse_args()
+    if args.counter_summary:
+        counter_summary(args.counter_summary, args.counter_config, args.counter_name,
+                        args.counter_commands)
+        return
     if args.trace_summary:
         trace_summary(args.trace_summary, args.trace_config)
         return

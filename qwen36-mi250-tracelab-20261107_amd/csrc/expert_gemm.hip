@@ -354,23 +354,15 @@ hipError_t launch_cfg(const Cfg& c, const GemmArgs& a, int grid, hipStream_t st)
   if (c.wr == WR && c.wk == WK && c.tokb == TOKB && c.kc == KCV && c.r == RV) {                \
     MOE_LAUNCH(WR, WK, TOKB, KCV, RV)                                                           \
   }
+  // the configurations the preference lists of launch_expert_gemm can reach
   if constexpr (HAS_FP8) {
     MOE_L(4, 1, 2, 256, 2)
-    MOE_L(2, 2, 2, 256, 2)
-    MOE_L(4, 2, 2, 256, 2)
-    MOE_L(2, 1, 2, 256, 2)
-    MOE_L(8, 1, 2, 256, 2)
     MOE_L(4, 1, 2, 128, 4)
-    MOE_L(1, 4, 1, 64, 8)
-    MOE_L(2, 2, 2, 64, 8)
-    MOE_L(2, 1, 2, 64, 8)
-    MOE_L(4, 1, 4, 64, 8)
-    MOE_L(1, 4, 1, 128, 4)
-    MOE_L(2, 2, 2, 128, 4)
     MOE_L(2, 1, 2, 128, 4)
-    MOE_L(4, 1, 4, 128, 4)
+    MOE_L(1, 4, 1, 64, 8)
     MOE_L(1, 2, 1, 128, 4)
     MOE_L(1, 1, 1, 128, 4)
+    MOE_L(4, 1, 4, 64, 8)
     MOE_L(4, 1, 8, 64, 4)
   } else {
     MOE_L(1, 8, 1, 64, 4)
@@ -381,10 +373,7 @@ hipError_t launch_cfg(const Cfg& c, const GemmArgs& a, int grid, hipStream_t st)
     MOE_L(4, 1, 8, 64, 4)
     MOE_L(1, 2, 1, 128, 4)
     MOE_L(1, 1, 1, 128, 4)
-    MOE_L(1, 4, 1, 128, 4)
-    MOE_L(2, 2, 2, 128, 4)
     MOE_L(2, 1, 2, 128, 4)
-    MOE_L(4, 1, 4, 128, 4)
     MOE_L(1, 1, 1, 32, 4)
     MOE_L(1, 1, 2, 32, 4)
     MOE_L(1, 1, 4, 32, 4)
@@ -425,7 +414,7 @@ hipError_t launch_expert_gemm(int mode, int role, int bm, const GemmArgs& a_in, 
   // fp8 weights move half the bytes per K element: 128-element chunks keep as many bytes
   // in flight as the bf16 64-element ones.
   const int rr = fp8 ? 8 : 4;  // fp8: 64-element chunks are half the bytes, twice as many
-  if (role == kRoleRouter && tokb == 1) prefs[n++] = {1, 8, 1, 64, rr};
+  if (role == kRoleRouter && tokb == 1 && !fp8) prefs[n++] = {1, 8, 1, 64, rr};
   if (tokb == 1) {
     prefs[n++] = {1, 4, 1, 64, rr};
     prefs[n++] = {1, 2, 1, 128};
