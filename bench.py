@@ -480,6 +480,62 @@ def pmc_summary(fetch_dir, write_dir, copy_mib, config):
     print(md.read_text())
 
 
+KERNEL_STATS_FILES = {"c2": ("moe_layer_c2_decode_b1_kernels",
+                              "C2: MoE layer, decode batch 1 (H2048 E256 top-8 + shared, bf16), 16 "
+                              "layers cycled"),
+                       "c3": ("moe_layer_c3_decode_b64_zipf_kernels",
+                              "C3: MoE layer, batch 64 with Zipf(1.1) routing (bf16), 16 layers "
+                              "cycled"),
+                       "c4": ("moe_layer_c4_prefill_4096_kernels",
+                              "C4: MoE layer, 4096-token prefill chunk (bf16), 4 layers cycled"),
+                       "c5": ("moe_layer_c5_fp8_b32_kernels",
+                              "C5: 40-layer stack, fp8-e4m3 routed experts, batch 32")}
+
+
+def kernel_stats_summary(prof_dir, config):
+    """The library's kernels in a `rocprofv3 --kernel-trace --stats` run of `bench.py
+    --configs <config> --no-cpu` (stdout of the run in <prof_dir>.json): calls and average /
+    min / max duration, ordered by total time. Written to profiles/moe_layer_<config>_*.md."""
+    import csv
+    import glob
+    import re
+
+    name, title = KERNEL_STATS_FILES[config]
+    f = glob.glob(os.path.join(prof_dir, "**", "*kernel_stats.csv"), recursive=True)[0]
+    rows = []
+    for r in csv.DictReader(open(f)):
+        n = r["Name"].replace("(anonymous namespace)::", "")
+        m = re.match(r"(?:void )?(moe::[A-Za-z0-9_]+(?:<[^>]*>)?)", n)
+        if m:
+            rows.append((m.group(1), int(r["Calls"]), float(r["AverageNs"]) / 1e3,
+                         float(r["MinNs"]) / 1e3, float(r["MaxNs"]) / 1e3,
+                         float(r["TotalDurationNs"])))
+    rows.sort(key=lambda x: -x[5])
+    lines = [f"# {title}\n",
+             "Command (run on one MI355X from the repository root; `cd /tmp && export "
+             "TMPDIR=/tmp` first, paths absolute):\n",
+             f"    rocprofv3 --kernel-trace --stats --output-format csv -d <out> -o run -- python3 "
+             f"bench.py --configs {config} --no-cpu > <out>.json",
+             f"    python3 bench.py --stats-summary <out> --stats-config {config}\n",
+             "Kernel statistics (rocprofv3 kernel_stats.csv; libmoe_mi355x.so kernels only; "
+             "microseconds). The run includes the untimed routing-statistics pass, graph warm-up "
+             "and the dominant-kernel (gate_up) graph (and, at C2, the graphs of the add + RMSNorm "
+             "side measurement), so call counts exceed the timed steps.\n",
+             "| kernel | calls | avg us | min us | max us |", "|---|---|---|---|---|"]
+    lines += [f"| `{k}` | {n} | {a:.2f} | {mi:.2f} | {ma:.2f} |" for k, n, a, mi, ma, _ in rows]
+    try:
+        line = json.loads(Path(prof_dir + ".json").read_text().strip().splitlines()[-1])
+        c = line["configs"][config]
+        lines += ["", f"Same run, bench line for {config} (timed under the profiler): "
+                      f"{c['us_per_layer']} us/layer, gate_up kernel `{c['gate_up_kernel']}` "
+                      f"{c['gate_up_us']} us per launch, {c['gate_up_GBps']} GB/s algorithmic."]
+    except (OSError, ValueError, KeyError):
+        pass
+    md = ROOT / "profiles" / f"{name}.md"
+    md.write_text("\n".join(lines) + "\n")
+    print(md.read_text())
+
+
 def counter_summary(dirs, config, name, commands):
     """Per-kernel medians of the SQ counters in one or more `rocprofv3 --pmc` runs (one
     counter set per run) of `bench.py --configs <config>`, for the launches of each kernel
@@ -637,6 +693,10 @@ def main():
                     help="summarise a rocprofv3 --kernel-trace run of `bench.py --configs c` "
                          "into profiles/timeline_<c>.md and exit")
     ap.add_argument("--trace-config", default="c2")
+    ap.add_argument("--stats-summary", metavar="PROF_DIR",
+                    help="summarise a rocprofv3 --kernel-trace --stats run of `bench.py "
+                         "--configs c` into profiles/moe_layer_<c>_*.md and exit")
+    ap.add_argument("--stats-config", default="c2")
     ap.add_argument("--counter-summary", nargs="+", metavar="PMC_DIR",
                     help="summarise rocprofv3 --pmc runs of `bench.py --configs c` into "
                          "profiles/<--counter-name>.md and exit")
@@ -645,6 +705,9 @@ def main():
     ap.add_argument("--counter-commands", nargs="*", default=[],
                     help="the rocprofv3 commands of the runs (quoted, for the summary)")
     args = ap.parse_args()
+    if args.stats_summary:
+        kernel_stats_summary(args.stats_summary, args.stats_config)
+        return
     if args.counter_summary:
         counter_summary(args.counter_summary, args.counter_config, args.counter_name,
                         args.counter_commands)
