@@ -40,7 +40,7 @@ struct GemmArgs {
   int topk, P, E, T;
   int nrb;           // weight-row blocks per tile (set by the launcher)
   int MTgrid;        // tiles the grid covers (set by the launcher)
-  int shared_first;  // prefill: the table's last shared_first tiles run first (launcher)
+  int shared_first;  // the table's last shared_first tiles run first (set by the launcher)
 };
 
 // Launches k_expert_gemm over max_tiles tiles of at most bm (16, 32, 64 or 128) sorted rows.

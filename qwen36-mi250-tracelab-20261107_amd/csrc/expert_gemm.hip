@@ -311,12 +311,20 @@ void k_expert_gemm(GemmArgs args) {
 
 
   const int nrb = args.nrb;
-  const int tile = blockIdx.x / nrb;
+  int tile = blockIdx.x / nrb;
   const int rb = blockIdx.x - tile * nrb;
 
   int e, r0, r1;
   if (args.table) {
-    if (tile >= args.table[3 * args.MT]) return;
+    const int ntiles = args.table[3 * args.MT];
+    if (tile >= ntiles) return;
+    if (args.shared_first > 0) {
+      // the shared expert's tiles (the table's last ones: every token of the batch, and in
+      // an fp8 launch bf16 rows of twice the bytes) are dispatched first, so that the
+      // longest workgroups do not start in the launch's last round
+      const int ns = min(args.shared_first, ntiles);
+      tile = tile < ns ? ntiles - ns + tile : tile - ns;
+    }
     e = args.table[tile];
     r0 = args.table[args.MT + tile];
     r1 = args.table[2 * args.MT + tile];
@@ -449,6 +457,11 @@ hipError_t launch_expert_gemm(int mode, int role, int bm, const GemmArgs& a_in, 
     int nmax = a.op[0].N > a.op[1].N ? a.op[0].N : a.op[1].N;
     a.nrb = nmax / rows;
     if (a.nrb <= 0 || max_tiles <= 0) return hipSuccess;
+    a.shared_first = 0;
+    if (a.table && a.op[0].N > 0 && a.op[1].N > 0) {
+      const char* env = knob(kKnobGemmSharedFirst);
+      if (!(env && env[0] == '0')) a.shared_first = (a.T + c.tokb * 16 - 1) / (c.tokb * 16);
+    }
     long long grid = (long long)max_tiles * a.nrb;
     if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
     hipError_t err;

@@ -414,7 +414,8 @@ namespace moe {
 namespace {
 const char* const kKnobNames[kKnobCount] = {"MOE_DECODE",       "MOE_DECODE_DOWN",
                                             "MOE_DECODE_GU_BLOCKS", "MOE_MIXED",
-                                            "MOE_PREFILL_SIDE", "MOE_PREFILL_SHARED_FIRST"};
+                                            "MOE_PREFILL_SIDE", "MOE_PREFILL_SHARED_FIRST",
+                                            "MOE_GEMM_SHARED_FIRST"};
 std::mutex g_knob_mu;
 std::atomic<bool> g_knobs_read{false};
 char g_knob_val[kKnobCount][32];

@@ -16,7 +16,8 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 constexpr int kWave = 64;
 
 // Comparison switches of the launch path (MOE_DECODE, MOE_DECODE_DOWN, MOE_DECODE_GU_BLOCKS,
-// MOE_MIXED, MOE_PREFILL_SIDE, MOE_PREFILL_SHARED_FIRST): each selects a variant that the
+// MOE_MIXED, MOE_PREFILL_SIDE, MOE_PREFILL_SHARED_FIRST,
+// MOE_GEMM_SHARED_FIRST): each selects a variant that the
 // GPU tests compare with the default. They are read from the environment once per process
 // and again by moe_reload_tuning(), never per launch.
 enum Knob {
@@ -26,6 +27,7 @@ enum Knob {
   kKnobMixed,
   kKnobPrefillSide,
   kKnobPrefillSharedFirst,
+  kKnobGemmSharedFirst,
   kKnobCount
 };
 // The switch's value, or nullptr when it is unset (host code).

@@ -139,6 +139,39 @@ def test_fp8_mixed_launch_matches_side_branch(pkg, dev, T):
     assert max_abs(a, b) <= 4e-3 * scale
 
 
+@pytest.mark.parametrize("fp8,T", [(False, 17), (False, 64), (False, 300), (True, 32),
+                                    (True, 200)])
+def test_gemm_shared_tile_order_agrees(pkg, dev, fp8, T):
+    """A tiled (expert GEMM) launch holding routed and shared tiles gives the same bits
+    whether the shared expert's tiles are dispatched first (the default) or in table order
+    (MOE_GEMM_SHARED_FIRST=0): every tile is computed the same way, only the dispatch order
+    differs. bf16 experts, and fp8 experts beside the bf16 shared expert in one launch."""
+    import __graft_entry__
+
+    Hh, E, I = 2048, 256, 512
+    gen = torch.Generator(device=dev).manual_seed(40 + T)
+
+    def rnd(*shape):
+        return (torch.randn(*shape, generator=gen, device=dev) * 0.02).to(BF16)
+
+    w = {"router": rnd(E, Hh), "gate_up": rnd(E, 2 * I, Hh), "down": rnd(E, Hh, I),
+         "sh_gate": rnd(I, Hh), "sh_up": rnd(I, Hh), "sh_down": rnd(Hh, I), "sh_gate_w": rnd(1, Hh)}
+    mlp = __graft_entry__._mlp_from_weights(w, dev)
+    if fp8:
+        q, s = pkg.fp8.quantize_rows(w["gate_up"])
+        q2, s2 = pkg.fp8.quantize_rows(w["down"])
+        mlp.experts.gate_up_proj, mlp.experts.gate_up_scale = q, s
+        mlp.experts.down_proj, mlp.experts.down_scale = q2, s2
+    x = torch.randn(T, Hh, generator=torch.Generator().manual_seed(T)).to(BF16).to(dev)
+    outs = []
+    for env in ({"MOE_GEMM_SHARED_FIRST": None}, {"MOE_GEMM_SHARED_FIRST": "0"}):
+        with knobs(**env):
+            for decode in (False, True):
+                outs.append(pkg.block.moe(x, mlp, 8, decode=decode))
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[2]) and torch.equal(outs[1], outs[3])
+
+
 def test_fp8_stack_of_layers_t32(pkg, dev):
     """C5 as a stack: four independent full-shape layers with fp8-e4m3 experts (each from
     its own bf16 N(0, 0.02) masters) at 32 tokens, in the bench's mode (decode=True: bf16
