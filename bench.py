@@ -565,7 +565,7 @@ def counter_summary(dirs, config, name, commands):
     counters = sorted({c for kv in vals.values() for c in kv})
     kernels = sorted(vals, key=lambda k: -max(statistics.median(v) for v in vals[k].values()))
     med = {k: {c: statistics.median(vals[k][c]) for c in vals[k]} for k in kernels}
-    lines = [f"# SQ counters of the {config} kernels\n",
+    lines = [f"# Counters of the {config} kernels\n",
              "Commands (from the repository root on one MI355X; `cd /tmp && export TMPDIR=/tmp` "
              "first, paths absolute; one counter set per run):\n"]
     lines += ["    " + c for c in commands]
@@ -590,7 +590,14 @@ def counter_summary(dirs, config, name, commands):
                ("SQ_INST_LEVEL_VMEM / SQ_WAVE_CYCLES (load instructions in flight per wave)",
                 "SQ_INST_LEVEL_VMEM", "SQ_WAVE_CYCLES"),
                ("SQ_VALU_MFMA_BUSY_CYCLES / SQ_BUSY_CYCLES", "SQ_VALU_MFMA_BUSY_CYCLES",
-                "SQ_BUSY_CYCLES")]
+                "SQ_BUSY_CYCLES"),
+               ("TCP_TCC_READ_REQ_LATENCY_sum / TCP_TCC_READ_REQ_sum (cycles from a vector L1 "
+                "miss to its L2 reply)", "TCP_TCC_READ_REQ_LATENCY_sum", "TCP_TCC_READ_REQ_sum"),
+               ("TCC_EA0_RDREQ_LEVEL_sum / TCC_EA0_RDREQ_sum (cycles from an L2 miss to its "
+                "memory reply)", "TCC_EA0_RDREQ_LEVEL_sum", "TCC_EA0_RDREQ_sum"),
+               ("TCC_HIT_sum / TCC_REQ_sum (L2 hit rate)", "TCC_HIT_sum", "TCC_REQ_sum"),
+               ("TCP_UTCL1_TRANSLATION_MISS_sum / TCP_UTCL1_REQUEST_sum (L1 TLB miss rate)",
+                "TCP_UTCL1_TRANSLATION_MISS_sum", "TCP_UTCL1_REQUEST_sum")]
     lines += ["", "| ratio | " + " | ".join(f"`{k}`" for k in kernels) + " |",
               "|---|" + "---|" * len(kernels)]
     for label, a, b in derived:
@@ -622,7 +629,8 @@ def trace_summary(trace_dir, config):
                 if "moe::" in r["Kernel_Name"]:
                     name = (r["Kernel_Name"].replace("void ", "")
                             .replace("(anonymous namespace)::", "").split("(")[0])
-                    rows.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), name))
+                    rows.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), name,
+                                 r.get("Queue_Id", "")))
     rows.sort()
     runs, cur = [], [rows[0]]
     for r in rows[1:]:
@@ -632,16 +640,39 @@ def trace_summary(trace_dir, config):
         cur.append(r)
     runs.append(cur)
     run = max(runs, key=len)
-    # the period starts at the router launch (the first kernel of a layer)
-    start = next((i for i, r in enumerate(run) if "router" in r[2]), 0)
-    run = run[start:]
-    first = run[0][2]
-    period = next((i for i in range(1, len(run)) if run[i][2] == first), len(run))
-    layers = [run[i:i + period] for i in range(0, len(run) - period + 1, period)
-              if [r[2] for r in run[i:i + period]] == [r[2] for r in run[:period]]]
+    # layers: from one router launch to the next (with the shared expert on the auxiliary
+    # stream the dispatch order inside a layer varies, so kernels are matched by name and
+    # occurrence, not by position)
+    # the routed chain's queue is the router's; a dispatch on another queue (the shared
+    # expert on the auxiliary stream, forked at the block's start just before the router, and
+    # the joining combine) belongs to the last layer whose router started at most 10 us after it
+    mainq = next((r[3] for r in run if "router" in r[2]), "")
+    rstarts = [r[0] for r in run if "router" in r[2]]
+    segs = [[] for _ in rstarts]
+    for r in run:
+        lead = 0 if r[3] == mainq else 10_000
+        i = max((j for j, t in enumerate(rstarts) if t <= r[0] + lead), default=-1)
+        if 0 <= i < len(segs):
+            segs[i].append(r)
+    segs = [sorted(sg) for sg in segs[:-1]]
+
+    def keyed(seg):
+        seen, out = {}, []
+        for r in seg:
+            seen[r[2]] = seen.get(r[2], 0) + 1
+            out.append((f"{r[2]}#{seen[r[2]]}", r[:3]))
+        return out
+
+    segs = [keyed(sg) for sg in segs]
+    ref = sorted(k for k, _ in segs[len(segs) // 2]) if segs else []
+    layers = [dict(sg) for sg in segs if sorted(k for k, _ in sg) == ref]
     layers = layers[1:-1] if len(layers) > 4 else layers  # drop the replay's ramp and tail
-    starts = [ly[0][0] for ly in layers]
+    starts = [min(r[0] for r in ly.values()) for ly in layers]
     per = statistics.median(b - a for a, b in zip(starts, starts[1:])) / 1e3 if len(starts) > 1 else 0
+    first = next(k for k, _ in segs[len(segs) // 2])
+    order = sorted(ref, key=lambda k: statistics.median(ly[k][0] - ly[first][0] for ly in layers))
+    period = len(order)
+    run = [r for ly in layers for r in ly.values()]
     lines = [f"# Timeline of one {config} layer in the timed graph replay\n",
              "Commands (from the repository root on one MI355X; `cd /tmp && export TMPDIR=/tmp` "
              "first, paths absolute):\n",
@@ -654,19 +685,37 @@ def trace_summary(trace_dir, config):
              "| # | kernel | start offset | duration | gap before (since previous dispatch ended) |",
              "|---|---|---|---|---|"]
     busy = 0.0
-    for i in range(period):
-        off = statistics.median((ly[i][0] - ly[0][0]) / 1e3 for ly in layers)
-        dur = statistics.median((ly[i][1] - ly[i][0]) / 1e3 for ly in layers)
-        if i:
-            gap = statistics.median((ly[i][0] - ly[i - 1][1]) / 1e3 for ly in layers)
-        else:
-            gap = statistics.median((layers[j][0][0] - layers[j - 1][-1][1]) / 1e3
-                                    for j in range(1, len(layers))) if len(layers) > 1 else 0.0
+    for i, k in enumerate(order):
+        off = statistics.median((ly[k][0] - min(r[0] for r in ly.values())) / 1e3 for ly in layers)
+        dur = statistics.median((ly[k][1] - ly[k][0]) / 1e3 for ly in layers)
+        gaps = []
+        for j, ly in enumerate(layers):
+            prev = [r[1] for r in ly.values() if r[0] < ly[k][0]]
+            if not prev and j:
+                prev = [r[1] for r in layers[j - 1].values()]
+            if prev:
+                gaps.append((ly[k][0] - max(prev)) / 1e3)
+        gap = statistics.median(gaps) if gaps else 0.0
         busy += dur
-        lines.append(f"| {i} | `{layers[0][i][2]}` | {off:.2f} | {dur:.2f} | {gap:.2f} |")
-    lines.append(f"\nSum of the medians of the kernel durations: {busy:.2f} us of the {per:.2f} us "
-                 f"period; the rest ({per - busy:.2f} us) is time between dispatches. A negative "
-                 "gap is an overlap (the next dispatch started before the previous ended).")
+        lines.append(f"| {i} | `{k.split('#')[0]}` | {off:.2f} | {dur:.2f} | {gap:.2f} |")
+
+    def covered(ly):  # time with at least one library kernel running
+        iv = sorted((r[0], r[1]) for r in ly.values())
+        tot, cs, ce = 0, iv[0][0], iv[0][1]
+        for a, b in iv[1:]:
+            if a > ce:
+                tot += ce - cs
+                cs, ce = a, b
+            else:
+                ce = max(ce, b)
+        return (tot + ce - cs) / 1e3
+
+    cov = statistics.median(covered(ly) for ly in layers) if layers else 0.0
+    lines.append(f"\nSum of the medians of the kernel durations: {busy:.2f} us; time with at "
+                 f"least one kernel running: {cov:.2f} us of the {per:.2f} us period (the rest, "
+                 f"{per - cov:.2f} us, is time between dispatches). A negative gap is an overlap "
+                 "(the dispatch started before the latest-ending earlier one ended: kernels on "
+                 "the auxiliary stream).")
     md = ROOT / "profiles" / f"timeline_{config}.md"
     md.write_text("\n".join(lines) + "\n")
     print(md.read_text())
