@@ -15,7 +15,7 @@ import pytest
 import torch
 
 from oracle import moe_oracle as orc
-from tests.helpers import BF16, knobs, max_abs, mean_rel
+from tests.helpers import BF16, knobs, max_abs, mean_rel, routing
 
 pytestmark = pytest.mark.gpu
 
@@ -70,7 +70,57 @@ def test_fp8_experts_match_dequantised_oracle(pkg, dev, n):
     assert max_abs(out, ref) <= 1e-3 and mean_rel(out, ref) <= 5e-3
 
 
-@pytest.mark.parametrize("T", [1, 32])
+@pytest.mark.parametrize("n", [600, 1500])
+@pytest.mark.parametrize("mode", ["uniform", "skewed", "one"])
+@pytest.mark.parametrize("shape", [(32, 256, 128, 8), (16, 2048, 1024, 4)])
+def test_fp8_prefill_tiles_match_dequantised_oracle(pkg, dev, n, mode, shape):
+    """More than 512 tokens with e4m3 experts: the prefill kernel's fp8 form (128-k DMA
+    chunks, each 256-row table tile taken as two 128-token halves) against the fp32 oracle on
+    the dequantised weights, at a small shape and at the model's hidden size with a doubled
+    intermediate; run twice, bit-identical."""
+    e, h, i, k = shape
+    assert pkg._lib.load().moe_tile_rows(n) == 256
+    w = orc.make_weights(h, e, i, i, seed=n)
+    q, s, q2, s2 = _fp8_weights(w)
+    g = torch.Generator().manual_seed(n + 3)
+    x = torch.randn(n, h, generator=g).to(BF16)
+    idx, wt = routing(n, e, k, mode, g)
+    args = (x.to(dev), idx.to(dev), wt.to(dev), q.to(dev), q2.to(dev))
+    kw = dict(round_products=False, gate_up_scale=s.to(dev), down_scale=s2.to(dev))
+    out = pkg.ops.experts(*args, **kw)
+    again = pkg.ops.experts(*args, **kw)
+    torch.cuda.synchronize()
+    ref = orc.sorted_experts(x.float(), idx, wt, orc.dequantize_rows(q, s),
+                             orc.dequantize_rows(q2, s2))
+    scale = max(1.0, ref.abs().max().item())
+    print(f"fp8 prefill n={n} {mode} {shape}: max {max_abs(out, ref):.3g} mean-rel "
+          f"{mean_rel(out, ref):.3g}", flush=True)
+    assert max_abs(out, ref) <= 2e-2 * scale and mean_rel(out, ref) <= 6e-3
+    assert torch.equal(out, again), "not deterministic"
+
+
+def test_fp8_prefill_grouped_with_bf16_shared(pkg, dev):
+    """One grouped prefill call holding e4m3 routed tiles and the bf16 shared expert's tiles
+    runs them as two launches of one stream (one weight type per kernel): the routed
+    activations equal a routed-only call's and the shared ones a bf16 call's, bit for bit."""
+    e, h, i, k, n = 32, 256, 128, 8, 700
+    w = orc.make_weights(h, e, i, i, seed=5)
+    q, s, _, _ = _fp8_weights(w)
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(n, h, generator=g).to(BF16).to(dev)
+    idx, _ = routing(n, e, k, "uniform", g)
+    sp = pkg.ops.sort_pairs(idx.to(dev), e, shared=True)
+    sp_r = pkg.ops.sort_pairs(idx.to(dev), e)
+    shared = (w["sh_gate"].to(dev), w["sh_up"].to(dev))
+    act, act_sh = pkg.ops.grouped_gate_up(x, k, q.to(dev), sp, scale=s.to(dev), shared=shared)
+    act_r = pkg.ops.grouped_gate_up(x, k, q.to(dev), sp_r, scale=s.to(dev))
+    _, act_sh_b = pkg.ops.grouped_gate_up(x, k, w["gate_up"].to(dev), sp, shared=shared)
+    torch.cuda.synchronize()
+    assert torch.equal(act, act_r)
+    assert torch.equal(act_sh, act_sh_b)
+
+
+@pytest.mark.parametrize("T", [1, 32, 1024])
 def test_fp8_block_full_shape(pkg, dev, T):
     """C5's layer shape: fp8 routed experts, bf16 router / shared expert."""
     import __graft_entry__
