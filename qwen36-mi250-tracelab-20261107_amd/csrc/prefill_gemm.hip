@@ -301,57 +301,29 @@ __global__ __launch_bounds__(kThreads, 1) void k_prefill_gemm(GemmArgs args) {
 
 // ---------------------------------------------------------------- fp8-e4m3 weights
 //
-// The same tile contract with e4m3 weight bytes (per-output-row fp32 scales on the fp32
-// accumulator): a DMA chunk is 128 k, i.e. still 128 bytes of each weight row, so the weight
-// stages keep the bf16 kernel's layout (256 rows x 128 B, XOR-swizzled 16-byte units) and
-// their HBM access pattern while carrying twice the K. The token rows (bf16) of a 128-k
-// chunk are 256 bytes each, so the token stages hold 128 tokens: a workgroup takes one
-// half of a table tile (up to 256 sorted rows), the two halves of a tile being consecutive
-// workgroups of one XCD, which stream the same weight rows together and share them in its
-// L2. A fragment of the weights is 8 bytes of one row read from LDS and widened to bf16 in
-// registers (exact), then v_mfma_f32_16x16x32_bf16 as in the bf16 kernel.
+// The same tiles (256 weight rows x up to 256 sorted rows) with e4m3 weight bytes and
+// per-output-row fp32 scales on the fp32 accumulator. A DMA chunk is 64 k as in the bf16
+// kernel, so the token-row stages are the bf16 kernel's (256 rows x 128 bytes), while a
+// weight stage is 256 rows x 64 bytes (16 KiB): the ring holds five of them (four chunks
+// requested ahead, 144 KiB of LDS in all). A weight DMA load of a wave fills 16 rows x 64
+// bytes; lane l writes physical 16-byte unit l & 3 of row l >> 2 of its group, holding
+// logical unit (l & 3) ^ ((row >> 1) & 3), which keeps the fragment reads (8 rows of one
+// 16-byte read group) conflict-free.
+//
+// The chunk's k order is permuted the same way in both operands (the same products are
+// summed): lane group kq reads weight unit kq (16 e4m3 bytes, one ds_read_b128) once per
+// chunk and feeds its first 8 bytes to the chunk's k-step 0 and its last 8 to k-step 1,
+// against token units 2 kq and 2 kq + 1. The weights are widened to bf16 in registers
+// (gfx950's scaled conversion, scale 1: exact) just before their MFMAs.
 namespace {
-constexpr int F8TOK = 128;                        // tokens per workgroup (half a table tile)
-constexpr int F8KC = 128;                         // K elements per DMA chunk
-constexpr int F8BRow = F8KC * 2;                  // token-row bytes per chunk: 256
+constexpr int F8RowBytes = DKC;                   // weight bytes of a row per chunk: 64
+constexpr int F8Stage = 256 * F8RowBytes;         // 16 KiB
+constexpr int F8StagesA = 5, F8AheadA = 4;
+constexpr int F8ALoads = 256 / 16 / 8;            // weight DMA loads per wave per chunk: 2
+constexpr int F8LdsBytes = F8StagesA * F8Stage + kStagesB * kOpStage;  // 144 KiB
+static_assert(F8AheadA == F8StagesA - 1, "weight ring: chunk d + S - 1 into chunk d - 1's stage");
 }  // namespace
 
-// Fragments of one double k-step (64 k) of a wave. The chunk's 128 k are read in a fixed
-// permutation that both operands share (the products summed are the same): lane group kq
-// of double step t takes weight unit 4 t + kq (16 e4m3 bytes, one conflict-free 16-byte LDS
-// read) and uses its first 8 bytes in k-step 2 t, its last 8 in k-step 2 t + 1; the token
-// fragments of those k-steps are the matching bf16 units 8 t + 2 kq and 8 t + 2 kq + 1.
-struct Frags8 {
-  u32x4v a[4];     // weight-row blocks, 16 e4m3 bytes each
-  u32x4v b[2][4];  // [k-step][token block 2 b + wn]
-};
-
-// astage: the lane's weight offset for the double step; bstage0 / bstage1: its token
-// offsets for the two k-steps.
-__device__ __forceinline__ void read_frags8(uint32_t astage, uint32_t bstage0, uint32_t bstage1,
-                                            Frags8& f) {
-  f.a[0] = lds_read_frag<0 * 16 * kRowBytes>(astage);
-  f.a[1] = lds_read_frag<1 * 16 * kRowBytes>(astage);
-  f.a[2] = lds_read_frag<2 * 16 * kRowBytes>(astage);
-  f.a[3] = lds_read_frag<3 * 16 * kRowBytes>(astage);
-  f.b[0][0] = lds_read_frag<0 * 32 * F8BRow>(bstage0);
-  f.b[0][1] = lds_read_frag<1 * 32 * F8BRow>(bstage0);
-  f.b[0][2] = lds_read_frag<2 * 32 * F8BRow>(bstage0);
-  f.b[0][3] = lds_read_frag<3 * 32 * F8BRow>(bstage0);
-  f.b[1][0] = lds_read_frag<0 * 32 * F8BRow>(bstage1);
-  f.b[1][1] = lds_read_frag<1 * 32 * F8BRow>(bstage1);
-  f.b[1][2] = lds_read_frag<2 * 32 * F8BRow>(bstage1);
-  f.b[1][3] = lds_read_frag<3 * 32 * F8BRow>(bstage1);
-}
-__device__ __forceinline__ void frags_ready8(Frags8& f) {
-  lds_frags_ready();
-#pragma unroll
-  for (int a = 0; a < 4; ++a) after_wait(f.a[a]);
-#pragma unroll
-  for (int h = 0; h < 2; ++h)
-#pragma unroll
-    for (int b = 0; b < 4; ++b) after_wait(f.b[h][b]);
-}
 // 8 e4m3 bytes -> bf16x8 (exact)
 __device__ __forceinline__ u32x4v widen8(uint32_t lo, uint32_t hi) {
   u32x4v r;
@@ -361,32 +333,75 @@ __device__ __forceinline__ u32x4v widen8(uint32_t lo, uint32_t hi) {
   r.w = fp8x2_to_bf16x2<true>(hi);
   return r;
 }
-__device__ __forceinline__ void mma_frags8(const Frags8& f, int nb, f32x4_t (&acc)[4][4]) {
+// Token fragments of one k-step (the wave's 8 blocks 2 b + wn) from the B stage at bstage.
+__device__ __forceinline__ void read_bfrags(uint32_t bstage, u32x4v (&b)[8]) {
+  b[0] = lds_read_frag<0 * kBlkBytes>(bstage);
+  b[1] = lds_read_frag<2 * kBlkBytes>(bstage);
+  b[2] = lds_read_frag<4 * kBlkBytes>(bstage);
+  b[3] = lds_read_frag<6 * kBlkBytes>(bstage);
+  b[4] = lds_read_frag<8 * kBlkBytes>(bstage);
+  b[5] = lds_read_frag<10 * kBlkBytes>(bstage);
+  b[6] = lds_read_frag<12 * kBlkBytes>(bstage);
+  b[7] = lds_read_frag<14 * kBlkBytes>(bstage);
+}
+// Weight fragments of one chunk (4 row blocks of 16 rows, 16 bytes per lane).
+__device__ __forceinline__ void read_afrags8(uint32_t astage, u32x4v (&a)[4]) {
+  a[0] = lds_read_frag<0 * 16 * F8RowBytes>(astage);
+  a[1] = lds_read_frag<1 * 16 * F8RowBytes>(astage);
+  a[2] = lds_read_frag<2 * 16 * F8RowBytes>(astage);
+  a[3] = lds_read_frag<3 * 16 * F8RowBytes>(astage);
+}
+template <int N>
+__device__ __forceinline__ void tie(u32x4v (&v)[N]) {
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    u32x4v a[4];
+  for (int i = 0; i < N; ++i) after_wait(v[i]);
+}
+// k-step h of a chunk: weight halves h of a[], token fragments b[], first nb blocks.
+__device__ __forceinline__ void mma8(const u32x4v (&a)[4], int h, const u32x4v (&b)[8], int nb,
+                                     f32x4_t (&acc)[4][8]) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      a[i] = h ? widen8(f.a[i].z, f.a[i].w) : widen8(f.a[i].x, f.a[i].y);
+  for (int i = 0; i < 4; ++i) {
+    const u32x4v w = h ? widen8(a[i].z, a[i].w) : widen8(a[i].x, a[i].y);
 #pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      if (b >= nb) break;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) acc[i][b] = mfma_frag(a[i], f.b[h][b], acc[i][b]);
+    for (int bb = 0; bb < 8; ++bb) {
+      if (bb >= nb) break;
+      acc[i][bb] = mfma_frag(w, b[bb], acc[i][bb]);
     }
   }
 }
 
-// One work item of the fp8 kernel: rows [r0, r1) (at most 128) of expert e against weight-row
-// block rb: the whole DMA / MFMA pipeline of one tile and its epilogue.
 template <int MODE>
-__device__ __forceinline__ void f8_item(const GemmArgs& args, int e, int r0, int r1,
-                                        int rb) {
+__global__ __launch_bounds__(kThreads, 1) void k_prefill_gemm_f8(GemmArgs args) {
+  extern __shared__ uint4 smem[];  // A ring [F8StagesA][16 KiB], B ring [kStagesB][32 KiB]
+
+  // tile / row-block order, table lookup and bounds: as k_prefill_gemm
+  const int nrb = args.nrb;
+  const int xcd = blockIdx.x & (kXcds - 1);
+  const int j = blockIdx.x / kXcds;
+  int tile = (j / nrb) * kXcds + xcd;
+  const int rb = j - (j / nrb) * nrb;
+  if (tile >= args.MTgrid) return;
+  int e, r0, r1;
+  if (args.table) {
+    const int ntiles = args.table[3 * args.MT];
+    if (tile >= ntiles) return;
+    if (args.shared_first > 0) {
+      const int ns = min(args.shared_first, ntiles);
+      tile = tile < ns ? ntiles - ns + tile : tile - ns;
+    }
+    e = args.table[tile];
+    r0 = args.table[args.MT + tile];
+    r1 = min(args.table[2 * args.MT + tile], r0 + PBM);
+  } else {
+    e = args.E;
+    r0 = args.P + tile * PBM;
+    if (r0 >= args.P + args.T) return;
+    r1 = min(r0 + PBM, args.P + args.T);
+  }
   const bool routed = e < args.E;
   const GemmOperand& op = routed ? args.op[0] : args.op[1];
   constexpr int kOutPerWG = MODE == kModeSwiglu ? PBN / 2 : PBN;
   if (rb * kOutPerWG >= op.N) return;
-  extern __shared__ uint4 smem[];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -397,21 +412,18 @@ __device__ __forceinline__ void f8_item(const GemmArgs& args, int e, int r0, int
   const int kq = lane >> 4;
   const int ntok = r1 - r0;
 
-  // ---- DMA sources. Weights: load i of the wave fills the 8-row group wave + 8 i of a
-  // stage (128 bytes of each row), lane l physical unit l & 7 of row l >> 3, holding logical
-  // unit (l & 7) ^ row. Token rows: load i fills the 4-row group wave + 8 i (256 bytes of
-  // each row), lane l physical unit l & 15 of row l >> 4, holding logical unit
-  // (l & 15) ^ (row & 15).
-  const uint8_t* __restrict__ srca[kLoadsPerWave];
+  // ---- DMA sources: weights (load i of the wave: 16-row group wave + 8 i), token rows (as
+  // k_prefill_gemm: 8-row group wave + 8 i, 128 bytes of each row)
+  const uint8_t* __restrict__ srca[F8ALoads];
   const uint16_t* __restrict__ srcb[kLoadsPerWave];
-  const uint8_t* __restrict__ wbase =
-      reinterpret_cast<const uint8_t*>(op.w) + (long long)(routed ? e : 0) * op.estride;
   {
-    const int grow = lane >> 3;
-    const int unit = (lane & 7) ^ grow;
+    const uint8_t* __restrict__ wbase =
+        reinterpret_cast<const uint8_t*>(op.w) + (long long)(routed ? e : 0) * op.estride;
+    const int arow = lane >> 2;
 #pragma unroll
-    for (int i = 0; i < kLoadsPerWave; ++i) {
-      const int row = (wave + 8 * i) * 8 + grow;  // 0..255
+    for (int i = 0; i < F8ALoads; ++i) {
+      const int row = (wave + 8 * i) * 16 + arow;  // 0..255
+      const int unit = (lane & 3) ^ ((row >> 1) & 3);
       long long wrow;
       if (MODE == kModeSwiglu) {
         const int g = rb * (PBN / 2) + (row >> 6) * 32 + (row & 31);
@@ -421,13 +433,11 @@ __device__ __forceinline__ void f8_item(const GemmArgs& args, int e, int r0, int
       }
       srca[i] = wbase + wrow + unit * 16;
     }
-  }
-  {
-    const int brow = lane >> 4;
+    const int grow = lane >> 3;
+    const int bunit = (lane & 7) ^ grow;
 #pragma unroll
     for (int i = 0; i < kLoadsPerWave; ++i) {
-      const int row = (wave + 8 * i) * 4 + brow;  // 0..127
-      const int unit = (lane & 15) ^ (row & 15);
+      const int row = (wave + 8 * i) * 8 + grow;
       const int r = min(r0 + row, r1 - 1);
       long long src;
       if (!routed)
@@ -436,60 +446,95 @@ __device__ __forceinline__ void f8_item(const GemmArgs& args, int e, int r0, int
         src = args.order[r] / args.topk;
       else
         src = r;
-      srcb[i] = op.in + src * op.ld_in + unit * 8;
+      srcb[i] = op.in + src * op.ld_in + bunit * 8;
     }
   }
   char* lds = reinterpret_cast<char*>(smem);
-  char* bring_lds = lds + kStagesA * kOpStage;
+  char* bring_lds = lds + F8StagesA * F8Stage;
   auto issue_a = [&](int d) {
-    char* st = lds + (d % kStagesA) * kOpStage;
+    char* st = lds + (d % F8StagesA) * F8Stage;
 #pragma unroll
-    for (int i = 0; i < kLoadsPerWave; ++i)
-      __builtin_amdgcn_global_load_lds(srca[i] + d * F8KC, st + (wave + 8 * i) * 1024, 16, 0,
-                                       kWeightCachePolicy);
+    for (int i = 0; i < F8ALoads; ++i)
+      __builtin_amdgcn_global_load_lds(srca[i] + d * F8RowBytes, st + (wave + 8 * i) * 1024, 16,
+                                       0, kWeightCachePolicy);
   };
   const int nb_loads = __builtin_amdgcn_readfirstlane(
-      min(kLoadsPerWave, max(0, ((ntok + 3) / 4 - wave + 7) / 8)));
+      min(kLoadsPerWave, max(0, ((r1 - r0 + 7) / 8 - wave + 7) / 8)));
   auto issue_b = [&](int d) {
     char* st = bring_lds + (d % kStagesB) * kOpStage;
 #pragma unroll
     for (int i = 0; i < kLoadsPerWave; ++i)
       if (i < nb_loads)
-        __builtin_amdgcn_global_load_lds(srcb[i] + d * F8KC, st + (wave + 8 * i) * 1024, 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(srcb[i] + d * DKC, st + (wave + 8 * i) * 1024, 16, 0, 0);
   };
-  // fragment offsets of this lane at k-step s of a chunk: weights row lr of a 16-row block,
-  // 8 bytes at k = 32 s + 8 kq (logical unit 2 s + kq / 2, half kq & 1); token row lr of a
-  // 16-row block, 16 bytes at logical unit 4 s + kq
   typedef __attribute__((address_space(3))) char lds_char;
   const uint32_t lds_base = (uint32_t)(uintptr_t)(lds_char*)lds;
-  uint32_t roa[2], rob[2][2];
-#pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    roa[t] = (uint32_t)(wm * 64 * kRowBytes + lr * kRowBytes + (((4 * t + kq) ^ (lr & 7)) * 16));
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-      rob[t][h] = (uint32_t)(wn * 16 * F8BRow + lr * F8BRow + (((8 * t + 2 * kq + h) ^ lr) * 16));
-  }
+  // weight fragment: row lr of a 16-row block, logical unit kq; token fragment of k-step h:
+  // row lr, logical unit 2 kq + h
+  const uint32_t ra = (uint32_t)(wm * 64 * F8RowBytes + lr * F8RowBytes +
+                                 ((kq ^ ((lr >> 1) & 3)) * 16));
+  const uint32_t rbo0 = (uint32_t)(wn * kBlkBytes + lr * kRowBytes + (((2 * kq) ^ (lr & 7)) * 16));
+  const uint32_t rbo1 =
+      (uint32_t)(wn * kBlkBytes + lr * kRowBytes + (((2 * kq + 1) ^ (lr & 7)) * 16));
 
-  f32x4_t acc[4][4];
+  f32x4_t acc[4][8];
 #pragma unroll
   for (int a = 0; a < 4; ++a)
 #pragma unroll
-    for (int b = 0; b < 4; ++b) acc[a][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int b = 0; b < 8; ++b) acc[a][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
   const int nblk = (ntok + 15) >> 4;
-  const int nb = __builtin_amdgcn_readfirstlane(min(4, (nblk - wn + 1) >> 1));
+  const int nb = __builtin_amdgcn_readfirstlane(min(8, (nblk - wn + 1) >> 1));
 
-  // Software pipeline as in the bf16 kernel, two double k-steps per chunk: at the first one
-  // of chunk d + 1 the wave issues B(d + 2) then A(d + 3).
-  const int nd = op.K / F8KC;
+  // Pipeline: chunk d's weight fragments are read at its k-step 0 and kept for k-step 1;
+  // the token fragments of each k-step are read while the previous one is multiplied. Load
+  // order: A(0 .. S - 3), B(0), A(S - 2), B(1), A(S - 1), then at chunk d + 1's first k-step
+  // B(d + 2), A(d + S), so that the loads younger than B(d) are exactly A(d + S - 2).
+  const int nd = op.K / DKC;
   const int nk = 2 * nd;
-  issue_a(0);
+  for (int d = 0; d < F8AheadA - 1; ++d)
+    if (d < nd) issue_a(d);
   if (nd > 0) issue_b(0);
-  if (nd > 1) issue_a(1);
+  if (F8AheadA - 1 < nd) issue_a(F8AheadA - 1);
   if (nd > 1) issue_b(1);
-  if (nd > 2) issue_a(2);
-  // the epilogue's row scales, requested now so that they arrive under the K loop
+  if (F8AheadA < nd) issue_a(F8AheadA);
+  // younger than B(0): A(S - 2), B(1), A(S - 1)
+  wait_loads(F8ALoads * (F8AheadA - 1 < nd) + nb_loads * (nd > 1) + F8ALoads * (F8AheadA < nd));
+  __builtin_amdgcn_s_barrier();
+  u32x4v acur[4], anxt[4], b0[8], b1[8];
+  read_afrags8(lds_base + ra, acur);
+  read_bfrags(lds_base + F8StagesA * F8Stage + rbo0, b0);
+  lds_frags_ready();
+  tie(acur);
+  tie(b0);
+  for (int d = 0; d < nd; ++d) {
+    const uint32_t bst = lds_base + F8StagesA * F8Stage + (d % kStagesB) * kOpStage;
+    // k-step 0 of chunk d (weights acur, tokens b0) while k-step 1's tokens are read
+    read_bfrags(bst + rbo1, b1);
+    mma8(acur, 0, b0, nb, acc);
+    lds_frags_ready();
+    tie(b1);
+    // k-step 1 while chunk d + 1's weights and k-step-0 tokens are read
+    const bool more = d + 1 < nd;
+    if (more) {
+      wait_loads(F8ALoads * (d + F8AheadA < nd));
+      __builtin_amdgcn_s_barrier();
+      if (d + 2 < nd) issue_b(d + 2);
+      if (d + 1 + F8AheadA < nd) issue_a(d + 1 + F8AheadA);
+      read_afrags8(lds_base + ((d + 1) % F8StagesA) * F8Stage + ra, anxt);
+      read_bfrags(lds_base + F8StagesA * F8Stage + ((d + 1) % kStagesB) * kOpStage + rbo0, b0);
+    }
+    mma8(acur, 1, b1, nb, acc);
+    if (more) {
+      lds_frags_ready();
+      tie(anxt);
+      tie(b0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acur[i] = anxt[i];
+    }
+  }
+
+  // ---- epilogue (k_prefill_gemm's), the row scales requested together first
   const float* sc = op.scale ? op.scale + (long long)(routed ? e : 0) * op.sstride : nullptr;
   float scl[4][4];
 #pragma unroll
@@ -503,37 +548,8 @@ __device__ __forceinline__ void f8_item(const GemmArgs& args, int e, int r0, int
         n = min(rb * PBN + wm * 64 + a * 16 + 4 * kq + i, op.N - 1);
       scl[a][i] = sc ? sc[n] : 1.f;
     }
-  Frags8 f0, f1;
-  wait_loads(4 * (nd > 1) + nb_loads * (nd > 1) + 4 * (nd > 2));
-  __builtin_amdgcn_s_barrier();
-  read_frags8(lds_base + roa[0], lds_base + kStagesA * kOpStage + rob[0][0],
-              lds_base + kStagesA * kOpStage + rob[0][1], f0);
-  frags_ready8(f0);
-  auto step = [&](int jj, Frags8& cur, Frags8& nxt) {
-    const bool more = jj + 1 < nk;
-    if (more) {
-      const int jn = jj + 1, dn = jn >> 1, tn = jn & 1;
-      if (tn == 0) {
-        wait_loads(4 * (dn + 1 < nd));
-        __builtin_amdgcn_s_barrier();
-        if (dn + kAheadB < nd) issue_b(dn + kAheadB);
-        if (dn + kAheadA < nd) issue_a(dn + kAheadA);
-      }
-      const uint32_t bst = lds_base + (kStagesA + dn % kStagesB) * kOpStage;
-      read_frags8(lds_base + (dn % kStagesA) * kOpStage + roa[tn], bst + rob[tn][0],
-                  bst + rob[tn][1], nxt);
-    }
-    mma_frags8(cur, nb, acc);
-    if (more) frags_ready8(nxt);
-  };
-  for (int jj = 0; jj < nk; jj += 2) {
-    step(jj, f0, f1);
-    step(jj + 1, f1, f0);
-  }
-
-  // ---- epilogue: lane (q = kq, j = lr) holds rows 4q..4q+3 of token column j per block.
 #pragma unroll
-  for (int b = 0; b < 4; ++b) {
+  for (int b = 0; b < 8; ++b) {
     if (b >= nb) break;
     const int rr = r0 + (2 * b + wn) * 16 + lr;
     if (rr >= r1) continue;
@@ -545,9 +561,8 @@ __device__ __forceinline__ void f8_item(const GemmArgs& args, int e, int r0, int
         float o[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          float g = acc[h][b][i] * scl[h][i], u = acc[2 + h][b][i] * scl[2 + h][i];
-          g = rbf(g);
-          u = rbf(u);
+          float g = rbf(acc[h][b][i] * scl[h][i]);
+          float u = rbf(acc[2 + h][b][i] * scl[2 + h][i]);
           o[i] = rbf(siluf_(g)) * u;
         }
         *reinterpret_cast<uint2*>(op.out + orow * op.ld_out + n) =
@@ -568,51 +583,6 @@ __device__ __forceinline__ void f8_item(const GemmArgs& args, int e, int r0, int
   }
 }
 
-// Persistent: one workgroup per CU (the LDS allows no more), each taking work items (tile,
-// row block, token half) in a fixed order until the table's tiles are done. Short items
-// (4 DMA chunks for the down projection) and the many empty halves would otherwise each
-// pay a workgroup dispatch. Item order: round r of the grid covers 4 S (tile, row block)
-// pairs p (S = workgroups per XCD); the two halves of a pair go to workgroups 8 apart, i.e.
-// to one XCD at the same time, where they share the weight rows in its L2.
-template <int MODE>
-__global__ __launch_bounds__(kThreads, 1) void k_prefill_gemm_f8(GemmArgs args) {
-  const int nrb = args.nrb;
-  const int xcd = blockIdx.x & (kXcds - 1);
-  const int slot = blockIdx.x / kXcds;
-  const int S = gridDim.x / kXcds;
-  const int half = slot & 1;
-  const int npairs = args.MTgrid * nrb;
-  const int ntiles = args.table ? args.table[3 * args.MT] : args.MTgrid;
-  for (int p = (slot >> 1) * kXcds + xcd; p < npairs; p += 4 * S) {
-    int tile = p / nrb;
-    const int rb = p - tile * nrb;
-    if (tile >= ntiles) break;  // the remaining items are past the table's tiles too
-    int e, r0, r1;
-    if (args.table) {
-      if (args.shared_first > 0) {
-        const int ns = min(args.shared_first, ntiles);
-        tile = tile < ns ? ntiles - ns + tile : tile - ns;
-      }
-      e = args.table[tile];
-      r0 = args.table[args.MT + tile];
-      r1 = min(args.table[2 * args.MT + tile], r0 + PBM);
-    } else {
-      e = args.E;
-      r0 = args.P + tile * PBM;
-      if (r0 >= args.P + args.T) break;
-      r1 = min(r0 + PBM, args.P + args.T);
-    }
-    r0 += half * F8TOK;
-    r1 = min(r1, r0 + F8TOK);
-    if (r0 >= r1) continue;
-    f8_item<MODE>(args, e, r0, r1, rb);
-    // the next item's loads refill the LDS stages: every wave is done with this item's
-    // (its epilogue stores drained too, so the next item's vmcnt waits count its own loads)
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-  }
-}
-
 int prefill_tile_rows() { return PBM; }
 
 bool prefill_fits(int mode, const GemmOperand& op) {
@@ -620,7 +590,7 @@ bool prefill_fits(int mode, const GemmOperand& op) {
   // SWIGLU: whole 128-row gate/up blocks; PLAIN: any multiple of 16 rows (the last block of
   // 256 may be partial); K in whole chunks of the fp8 kernel
   const bool rows_ok = mode == kModeSwiglu ? op.N % (PBN / 2) == 0 : op.N % 16 == 0;
-  return rows_ok && (op.fp8 ? op.K % F8KC == 0 : op.K % PKC == 0);
+  return rows_ok && (op.fp8 ? op.K % DKC == 0 : op.K % PKC == 0);
 }
 
 namespace {
@@ -665,28 +635,21 @@ hipError_t launch_prefill_gemm(int mode, const GemmArgs& a_in, int max_tiles, hi
     const char* env = knob(kKnobPrefillSharedFirst);
     if (!(env && env[0] == '0')) a.shared_first = (a.T + PBM - 1) / PBM;
   }
-  long long grid = (long long)((max_tiles + kXcds - 1) / kXcds) * kXcds * a.nrb;
-  if (f8) {
-    // persistent: one workgroup per CU, a whole number of pairs of workgroups per XCD
-    int dev = 0, cus = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-      return hipErrorInvalidDevice;
-    grid = (long long)((cus + 2 * kXcds - 1) / (2 * kXcds)) * 2 * kXcds;
-  }
+  const long long grid = (long long)((max_tiles + kXcds - 1) / kXcds) * kXcds * a.nrb;
   if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
+  const size_t lds_k = f8 ? (size_t)F8LdsBytes : lds;
   const void* fn = mode == kModeSwiglu
                        ? (f8 ? reinterpret_cast<const void*>(&k_prefill_gemm_f8<kModeSwiglu>)
                              : reinterpret_cast<const void*>(&k_prefill_gemm<kModeSwiglu>))
                        : (f8 ? reinterpret_cast<const void*>(&k_prefill_gemm_f8<kModePlain>)
                              : reinterpret_cast<const void*>(&k_prefill_gemm<kModePlain>));
-  hipError_t err = allow_lds(fn, mode + (f8 ? 2 : 0), (int)lds);
+  hipError_t err = allow_lds(fn, mode + (f8 ? 2 : 0), (int)lds_k);
   if (err != hipSuccess) return err;
   if (f8) {
     if (mode == kModeSwiglu)
-      hipLaunchKernelGGL(k_prefill_gemm_f8<kModeSwiglu>, dim3((unsigned)grid), dim3(kThreads), lds, st, a);
+      hipLaunchKernelGGL(k_prefill_gemm_f8<kModeSwiglu>, dim3((unsigned)grid), dim3(kThreads), lds_k, st, a);
     else
-      hipLaunchKernelGGL(k_prefill_gemm_f8<kModePlain>, dim3((unsigned)grid), dim3(kThreads), lds, st, a);
+      hipLaunchKernelGGL(k_prefill_gemm_f8<kModePlain>, dim3((unsigned)grid), dim3(kThreads), lds_k, st, a);
     return hipGetLastError();
   }
   if (mode == kModeSwiglu)
