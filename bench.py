@@ -32,7 +32,7 @@ sys.path.insert(0, str(ROOT))
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 H, E, K_TOP, I, IS = 2048, 256, 8, 512, 512
-SEEDS = {"c2": 1000, "c3": 2000, "c4": 3000, "c5": 4000}
+SEEDS = {"c2": 1000, "c3": 2000, "c4": 3000, "c5": 4000, "c4f8": 5000}
 METRIC = json.loads((ROOT / "BASELINE.json").read_text())["metric"] if (ROOT / "BASELINE.json").exists() \
     else "MoE layer us + achieved HBM TB/s (% peak), E=256 top-8 h=2048, batch 1/64"
 
@@ -281,7 +281,7 @@ def run_config(torch, dev, name, T, layers, steps, warmup, zipf=False, fp8=False
     us_k = ms * 1000.0 / (reps * layers)
     kbytes = sum(gate_up_bytes(d, T, fp8, logits=decode) for d in Ds) / len(Ds)
     res["gate_up_kernel"] = "k_dec_gate_up" if decode else (
-        "k_prefill_gemm" if T > 512 and not fp8 else "k_expert_gemm")
+        ("k_prefill_gemm_f8" if fp8 else "k_prefill_gemm") if T > 512 else "k_expert_gemm")
     res["gate_up_us"] = round(us_k, 3)
     res["gate_up_bytes"] = int(kbytes)
     res["gate_up_GBps"] = round(kbytes / (us_k * 1e-6) / 1e9, 1)
@@ -726,7 +726,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=32)
-    ap.add_argument("--configs", default="c2,c3,c4,c5,batches")
+    ap.add_argument("--configs", default="c2,c3,c4,c5,c4f8,batches")
     ap.add_argument("--layers", type=int, default=16)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -801,6 +801,10 @@ def main():
     if "c5" in cfgs:
         results["c5"] = run_config(torch, dev, "c5", 32, 40, max(40, args.steps // 40 * 40),
                                    40, fp8=True)
+    if "c4f8" in cfgs:
+        # not a BASELINE config: C4's prefill chunk with C5's fp8-e4m3 experts
+        results["c4f8"] = run_config(torch, dev, "c4f8", 4096, 4, max(8, args.steps // 32),
+                                     max(4, args.warmup // 8), fp8=True)
     if "batches" in cfgs:
         results["batches"] = small_batches(torch, dev)
     workloads = {k: v for k, v in results.items() if k != "batches"}
