@@ -62,8 +62,8 @@ const char* moe_last_error(void);
 void moe_reload_tuning(void);
 
 /* Sorted rows per tile (bm) the fused entry points use for T tokens: 16 for one token,
- * 32 up to 512, above that 256 (the prefill tiles: bf16 weights, hidden a multiple of 256,
- * intermediates of 128) or else 64. A table passed to moe_grouped_gate_up /
+ * 32 up to 512, above that 256 (the prefill tiles, bf16 or fp8-e4m3 weights: hidden a
+ * multiple of 256, intermediates of 128) or else 64. A table passed to moe_grouped_gate_up /
  * moe_grouped_down must be built with a bm of 16, 32, 64, 128 or 256. */
 int moe_tile_rows(int T);
 
