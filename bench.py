@@ -489,7 +489,10 @@ KERNEL_STATS_FILES = {"c2": ("moe_layer_c2_decode_b1_kernels",
                        "c4": ("moe_layer_c4_prefill_4096_kernels",
                               "C4: MoE layer, 4096-token prefill chunk (bf16), 4 layers cycled"),
                        "c5": ("moe_layer_c5_fp8_b32_kernels",
-                              "C5: 40-layer stack, fp8-e4m3 routed experts, batch 32")}
+                              "C5: 40-layer stack, fp8-e4m3 routed experts, batch 32"),
+                       "c4f8": ("moe_layer_c4f8_prefill_4096_fp8_kernels",
+                                "C4's 4096-token prefill chunk with fp8-e4m3 routed experts "
+                                "(not a BASELINE config), 4 layers cycled")}
 
 
 def kernel_stats_summary(prof_dir, config):
