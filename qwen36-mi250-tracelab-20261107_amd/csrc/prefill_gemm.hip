@@ -437,8 +437,13 @@ __global__ __launch_bounds__(kThreads, 1) void k_prefill_gemm_f8(GemmArgs args) 
       }
       srca[i] = wbase + wrow + unit * 16;
     }
+    // token rows: physical unit q = (l & 7) ^ row holds logical unit 2 (q & 3) + (q >> 2), so
+    // that the units 2 kq + h that k-step h reads sit where the bf16 kernel's k-step reads
+    // them (physical (4 h + kq) ^ row): that pattern is conflict-free, 2 kq + h at the
+    // physical unit was not (3.2 bank-conflict cycles per LDS instruction)
     const int grow = lane >> 3;
-    const int bunit = (lane & 7) ^ grow;
+    const int bq = (lane & 7) ^ grow;
+    const int bunit = 2 * (bq & 3) + (bq >> 2);
 #pragma unroll
     for (int i = 0; i < kLoadsPerWave; ++i) {
       const int row = (wave + 8 * i) * 8 + grow;
@@ -474,12 +479,11 @@ __global__ __launch_bounds__(kThreads, 1) void k_prefill_gemm_f8(GemmArgs args) 
   typedef __attribute__((address_space(3))) char lds_char;
   const uint32_t lds_base = (uint32_t)(uintptr_t)(lds_char*)lds;
   // weight fragment: row lr of a 16-row block, logical unit kq; token fragment of k-step h:
-  // row lr, logical unit 2 kq + h
+  // row lr, logical unit 2 kq + h (stored at physical (4 h + kq) ^ row)
   const uint32_t ra = (uint32_t)(wm * 64 * F8RowBytes + lr * F8RowBytes +
                                  ((kq ^ ((lr >> 1) & 3)) * 16));
-  const uint32_t rbo0 = (uint32_t)(wn * kBlkBytes + lr * kRowBytes + (((2 * kq) ^ (lr & 7)) * 16));
-  const uint32_t rbo1 =
-      (uint32_t)(wn * kBlkBytes + lr * kRowBytes + (((2 * kq + 1) ^ (lr & 7)) * 16));
+  const uint32_t rbo0 = (uint32_t)(wn * kBlkBytes + lr * kRowBytes + ((kq ^ (lr & 7)) * 16));
+  const uint32_t rbo1 = (uint32_t)(wn * kBlkBytes + lr * kRowBytes + (((4 + kq) ^ (lr & 7)) * 16));
 
   f32x4_t acc[4][8];
 #pragma unroll
