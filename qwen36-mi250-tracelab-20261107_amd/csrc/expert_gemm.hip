@@ -45,8 +45,12 @@ template <int MODE, int WR, int WK, int TOKB, bool HAS_FP8, int KC, int R>
 __device__ __forceinline__ void gemm_tile(const GemmArgs& args, uint4* __restrict__ lds, int e,
                                           int r0, int r1, int rb) {
   constexpr int kRowU4 = KC / 8;        // uint4 per staged token-row chunk (bf16)
-  // LDS row pitch in uint4: +2 for 128-byte rows, +1 for longer ones (measured fastest)
-  constexpr int kPitchU4 = kRowU4 + (kRowU4 == 8 ? 2 : 1);
+  // LDS row pitch in 16-byte units: 2 more than the row, so that it is 2 mod 4. Measured on
+  // gfx950 with a one-wave probe of the MFMA B read (lane: row l % 16, unit kq = l / 16):
+  // conflict-free for pitches 10, 14, 18, 22, 26, 34, 42 units, 3.8 conflict cycles per
+  // ds_read_b128 for every odd pitch and every multiple of 4 (11-26 for multiples of 8), and
+  // for any pitch when a k-step's units are not consecutive across kq (see ppart below).
+  constexpr int kPitchU4 = kRowU4 + 2;
   constexpr int LPC16 = KC / 32;        // bf16 weight loads per lane per chunk
   constexpr int LPC8 = KC / 64;         // fp8 weight loads per lane per chunk
   constexpr int LPCA = HAS_FP8 ? LPC8 : LPC16;  // ring entries per chunk (16-byte loads)
@@ -128,7 +132,12 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& args, uint4* __restric
   // Only the tile's real token rows are staged: the LDS rows past them keep stale data,
   // which reaches only MFMA output columns that are never stored.
   uint4* bsl = lds + wk * 2 * kBufU4;  // this K slice's two buffers
-  auto stage_slot = [&](int i) { return ((i * WR + wr) * RPI + qlane) * kPitchU4 + part; };
+  // fp8 tiles: the k-steps read token units 8 s + 2 kq + h (h = 0, 1: the two halves of a
+  // lane's 16 weight bytes); each is stored at 8 s + 4 h + kq, so that one k-step's reads
+  // are consecutive units across kq, as in the bf16 tiles (read at 8 s + 2 kq + h directly,
+  // each read costs 3.8 bank-conflict cycles at any pitch)
+  const int ppart = use_fp8 ? ((part & ~7) | ((part & 1) << 2) | ((part >> 1) & 3)) : part;
+  auto stage_slot = [&](int i) { return ((i * WR + wr) * RPI + qlane) * kPitchU4 + ppart; };
 
   // Load stream per chunk m (vmcnt retires in order): A(m) then B(m + 1), each issued R
   // chunks ahead, so waiting for one chunk's data never drains the rest of the ring.
@@ -186,9 +195,10 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& args, uint4* __restric
           if (tb < ntb) {
             const uint4* brow = bcur + (tb * 16 + lr) * kPitchU4;
             if (use_fp8) {
-              // fp8 A lane kq holds k = s*64 + kq*16 + h*8 (+0..7)
-              acc[tb] = mfma16x16x32(a0, brow[s * 8 + kq * 2], acc[tb]);
-              acc[tb] = mfma16x16x32(a1, brow[s * 8 + kq * 2 + 1], acc[tb]);
+              // fp8 A lane kq holds k = s*64 + kq*16 + h*8 (+0..7): token unit 8 s + 2 kq + h,
+              // stored at 8 s + 4 h + kq
+              acc[tb] = mfma16x16x32(a0, brow[s * 8 + kq], acc[tb]);
+              acc[tb] = mfma16x16x32(a1, brow[s * 8 + 4 + kq], acc[tb]);
             } else {
               acc[tb] = mfma16x16x32(a0, brow[s * 4 + kq], acc[tb]);
             }
@@ -302,7 +312,7 @@ __global__ __launch_bounds__(64 * WR * WK)
 __attribute__((amdgpu_waves_per_eu(gemm_waves_per_eu(WR, TOKB, HAS_FP8, KC, R))))
 void k_expert_gemm(GemmArgs args) {
   constexpr int kRowU4 = KC / 8;
-  constexpr int kPitchU4 = kRowU4 + (kRowU4 == 8 ? 2 : 1);
+  constexpr int kPitchU4 = kRowU4 + 2;
   constexpr int kBufU4 = TOKB * 16 * kPitchU4;
   constexpr int BM = 16 * TOKB;
   // LDS: [WK][2 buffers][TOKB*16 rows][pitch] uint4 at this KC (the larger of the two
@@ -452,7 +462,7 @@ hipError_t launch_expert_gemm(int mode, int role, int bm, const GemmArgs& a_in, 
   for (int i = 0; i < n; ++i) {
     const Cfg& c = prefs[i];
     if (!fits(c, mode, a.op[0]) || !fits(c, mode, a.op[1])) continue;
-    if (c.wk * 2 * c.tokb * 16 * (c.kc / 8 + (c.kc == 64 ? 2 : 1)) * 16 > 65536) continue;
+    if (c.wk * 2 * c.tokb * 16 * (c.kc / 8 + 2) * 16 > 65536) continue;
     int rows = (mode == kModeSwiglu ? 8 : 16) * c.wr;
     int nmax = a.op[0].N > a.op[1].N ? a.op[0].N : a.op[1].N;
     a.nrb = nmax / rows;
