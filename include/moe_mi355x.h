@@ -131,9 +131,8 @@ int moe_combine(const void* y, const void* w, int T, int H, int k, const void* y
 /* Decode stages (T <= 4 tokens; H 512, 1024, 2048 or 4096, I and IS 512 or 1024,
  * E <= 512, T*k <= 64): the three launches of engine/fast/fused.py's FusedDecode._moe
  * (fused.py:887-932). moe_decode_fits says whether a shape fits this path; the fused
- * entry points below take it on their own for such shapes with bf16 experts, and with
- * fp8 experts up to 2 tokens (the tiled path is faster above; MOE_DECODE=0 turns the
- * decode path off). */
+ * entry points below take it on their own for such shapes, with bf16 or fp8-e4m3 experts
+ * (MOE_DECODE=0 turns the decode path off). */
 int moe_decode_fits(int T, int H, int E, int k, int I, int IS);
 
 /* Stage 1: router logits [T, n_pack] (as moe_router_logits) and, with sh_gate / sh_up

@@ -95,9 +95,13 @@ bool decode_enabled() {
 
 // Whether the decode kernels take T tokens (given that the shape fits them): measured per
 // layer (16 layers cycled) against the tiled path with 32-row tiles, bf16 decode
-// 17.6 / 31.2 / 52.8 / 67.6 µs at 1 / 2 / 3 / 4 tokens against 43.9 / 49.3 / 58.6 / 68.7,
-// fp8 17.1 / 35.0 / 60.3 / 78.4 against 47.1 / 50.2 / 52.6 / 56.2: fp8 up to 2 tokens.
-bool decode_takes(int T, bool fp8) { return decode_enabled() && T <= (fp8 ? 2 : kDecMaxTokens); }
+// 17.6 / 31.2 / 52.8 / 67.6 µs at 1 / 2 / 3 / 4 tokens against 43.9 / 49.3 / 58.6 / 68.7;
+// fp8 at 4 tokens, since the several-row-block gate_up kernel, 47.7-47.9 against 56.9-57.1
+// (8 layers cycled): both weight types up to kDecMaxTokens.
+bool decode_takes(int T, bool fp8) {
+  (void)fp8;
+  return decode_enabled() && T <= kDecMaxTokens;
+}
 
 // A grouped prefill launch with routed and shared tiles: one launch, the shared expert's
 // tiles dispatched first (grouped gate_up at C4 303-310 against 317 µs with the shared

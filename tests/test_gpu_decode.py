@@ -120,7 +120,7 @@ def test_decode_experts_forward(pkg, dev, n, mode, shape):
     assert max_abs(got, tiled) <= 8e-3 * scale
 
 
-@pytest.mark.parametrize("T", [1, 4])
+@pytest.mark.parametrize("T", [1, 2, 3, 4])
 def test_decode_fp8_block(pkg, dev, layer, T):
     """fp8-e4m3 routed experts on the decode path against the dequantised fp32 oracle and
     the tiled fp8 path."""
