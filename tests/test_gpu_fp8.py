@@ -120,6 +120,35 @@ def test_fp8_prefill_grouped_with_bf16_shared(pkg, dev):
     assert torch.equal(act_sh, act_sh_b)
 
 
+@pytest.mark.parametrize("n", [2, 3, 4])
+def test_fp8_experts_decode_shape_match_dequantised_oracle(pkg, dev, n):
+    """The experts surface with fp8-e4m3 experts at the model's shape and 2-4 tokens, where
+    it takes the decode kernels, against the dequantised fp32 oracle (bf16 routing-weight
+    products, as the batched path rounds them)."""
+    H, E, K, I = 2048, 256, 8, 512
+    w = orc.make_weights(H, E, I, I, seed=30 + n)
+    q, s, q2, s2 = _fp8_weights(w)
+    assert pkg.ops.decode_fits(n, H, E, K, I, I)
+    g = torch.Generator().manual_seed(n)
+    x = torch.randn(n, H, generator=g).to(BF16)
+    logits = torch.nn.functional.linear(x, w["router"])
+    tw, ti = orc.route(logits, K)
+    out = pkg.ops.experts(x.to(dev), ti.to(dev), tw.to(dev), q.to(dev), q2.to(dev),
+                          round_products=True, gate_up_scale=s.to(dev), down_scale=s2.to(dev))
+    torch.cuda.synchronize()
+    deq_gu, deq_dn = orc.dequantize_rows(q, s), orc.dequantize_rows(q2, s2)
+    ref = torch.zeros(n, H)
+    for t in range(n):
+        for j in range(K):
+            e = int(ti[t, j])
+            gu = deq_gu[e] @ x[t].float()
+            a = torch.nn.functional.silu(gu[:I]) * gu[I:]
+            ref[t] += tw[t, j].float() * (deq_dn[e] @ a)
+    print(f"fp8 experts decode shape n={n}: max {max_abs(out, ref):.3g} mean-rel "
+          f"{mean_rel(out, ref):.3g}", flush=True)
+    assert max_abs(out, ref) <= 2e-2 and mean_rel(out, ref) <= 6e-3
+
+
 @pytest.mark.parametrize("T", [1, 32, 1024])
 def test_fp8_block_full_shape(pkg, dev, T):
     """C5's layer shape: fp8 routed experts, bf16 router / shared expert."""
