@@ -74,10 +74,11 @@ def test_fp8_experts_match_dequantised_oracle(pkg, dev, n):
 @pytest.mark.parametrize("mode", ["uniform", "skewed", "one"])
 @pytest.mark.parametrize("shape", [(32, 256, 128, 8), (16, 2048, 1024, 4)])
 def test_fp8_prefill_tiles_match_dequantised_oracle(pkg, dev, n, mode, shape):
-    """More than 512 tokens with e4m3 experts: the prefill kernel's fp8 form (128-k DMA
-    chunks, each 256-row table tile taken as two 128-token halves) against the fp32 oracle on
-    the dequantised weights, at a small shape and at the model's hidden size with a doubled
-    intermediate; run twice, bit-identical."""
+    """More than 512 tokens with e4m3 experts: the prefill kernel's fp8 form (64-k DMA
+    chunks, 256-row table tiles; experts of more than 256 rows span several tiles in the
+    skewed and one-expert modes) against the fp32 oracle on the dequantised weights, at a
+    small shape and at the model's hidden size with a doubled intermediate; run twice,
+    bit-identical."""
     e, h, i, k = shape
     assert pkg._lib.load().moe_tile_rows(n) == 256
     w = orc.make_weights(h, e, i, i, seed=n)
