@@ -319,6 +319,59 @@ def small_batches(torch, dev, layers=8, reps=20):
     return out
 
 
+def hbm_ceiling(torch, dev, gib=4, reps=10):
+    """What library streaming kernels reach on this HBM, as a practical ceiling beside the
+    8 TB/s peak: torch's sum over a gib-GiB bf16 tensor (reads only) and torch's copy of
+    gib/2 GiB into another tensor (reads and writes gib GiB in all). Best of 5 timings of
+    reps calls each, eager (the calls are milliseconds long)."""
+    n = (gib << 30) // 2
+    x = torch.empty(n, dtype=torch.bfloat16, device=dev).normal_()
+    out = {}
+
+    def best(fn, nbytes):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        t = []
+        for _ in range(5):
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            a.record()
+            for _ in range(reps):
+                fn()
+            b.record()
+            torch.cuda.synchronize()
+            t.append(a.elapsed_time(b) / reps)
+        return round(nbytes / (min(t) * 1e-3) / 1e12, 3)
+
+    out["read_sum_TBps"] = best(lambda: x.sum(), n * 2)
+    # the probe library's plain streaming read (probe/stream_read.hip), over grid sizes
+    import ctypes
+
+    lib = ctypes.CDLL(str(ROOT / "qwen36-mi250-tracelab-20261107_amd" / "libmoe_probe.so"))
+    fn = lib.moe_probe_stream_read
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_longlong, ctypes.c_void_p, ctypes.c_int,
+                   ctypes.c_void_p]
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    sink = torch.empty(16384 * 256, dtype=torch.int32, device=dev)
+    probe = {}
+    for blocks in (1024, 2048, 4096, 8192, 16384):
+        def read(b=blocks):
+            if fn(x.data_ptr(), n * 2, sink.data_ptr(), b, stream) != 0:
+                raise RuntimeError("moe_probe_stream_read failed")
+        probe[str(blocks)] = best(read, n * 2)
+    out["read_probe_TBps"] = max(probe.values())
+    out["read_probe_by_workgroups"] = probe
+    half = x[: n // 2]
+    dst = torch.empty_like(half)
+    out["copy_TBps"] = best(lambda: dst.copy_(half), n * 2)
+    out["GiB_per_call"] = gib
+    del x, dst
+    torch.cuda.synchronize()
+    return out
+
+
 def cpu_baseline(torch, seconds):
     """The CPU torch restatement of the reference path (oracle.block_bf16: Transformers
     block with batched_mm experts, engine/experts.py) on C2, timed on this host."""
@@ -754,6 +807,9 @@ def main():
                          "profiles/<--counter-name>.md and exit")
     ap.add_argument("--counter-config", default="c4")
     ap.add_argument("--counter-name", default="counters")
+    ap.add_argument("--hbm-ceiling", action="store_true",
+                    help="print the read (torch sum) and copy rates of library streaming "
+                         "kernels on this GPU as one JSON line and exit")
     ap.add_argument("--counter-commands", nargs="*", default=[],
                     help="the rocprofv3 commands of the runs (quoted, for the summary)")
     args = ap.parse_args()
@@ -781,6 +837,9 @@ def main():
         print("bench.py needs a HIP device", file=sys.stderr)
         sys.exit(1)
     dev = torch.device("cuda:0")
+    if args.hbm_ceiling:
+        print(json.dumps({"hbm_ceiling": hbm_ceiling(torch, dev), "peak_TBps": HBM_PEAK_GBS / 1e3}))
+        return
     pkg = load_pkg()
     pkg._lib.load()
     cfgs = [c.strip() for c in args.configs.split(",") if c.strip()]

@@ -17,6 +17,8 @@ from pathlib import Path
 HERE = Path(__file__).resolve().parent
 CSRC = HERE / "csrc"
 LIB = HERE / "libmoe_mi355x.so"
+PROBE = HERE / "probe"
+PROBE_LIB = HERE / "libmoe_probe.so"
 BUILD = HERE.parent / "_build" / "csrc"
 ARCH = os.environ.get("MOE_OFFLOAD_ARCH", "gfx950")
 
@@ -66,7 +68,24 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
     os.replace(tmp, LIB)
     if verbose:
         print(f"built {LIB} from {len(sources)} sources")
+    build_probe(verbose)
     return LIB
+
+
+def build_probe(verbose: bool = False) -> Path:
+    """The measurement probe (probe/*.hip) as its own libmoe_probe.so: bench.py's HBM
+    read ceiling; the MoE path neither links nor loads it."""
+    sources = sorted(PROBE.glob("*.hip"))
+    objs = [_compile(src) for src in sources]
+    tmp = PROBE_LIB.with_suffix(".so.tmp")
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"probe link failed:\n{res.stderr}")
+    os.replace(tmp, PROBE_LIB)
+    if verbose:
+        print(f"built {PROBE_LIB} from {len(sources)} sources")
+    return PROBE_LIB
 
 
 if __name__ == "__main__":

@@ -156,3 +156,21 @@ def test_noalloc_rejects_calls_beyond_its_scratch_before_any_launch(pkg):
     rc = lib.moe_block_forward_noalloc(None, -1, H, E, K, I, I, None, NP, None, None, None, None,
                                        0, None, None, None, None, 0, None, None, None, None, None)
     assert rc == pkg._lib.MOE_EINVAL
+
+
+def test_probe_library_loads():
+    """bench.py's read-ceiling probe is built beside the MoE library and exports its entry;
+    it rejects bad arguments on the host (no GPU call)."""
+    import ctypes
+    from pathlib import Path
+
+    path = Path(__file__).resolve().parent.parent / "qwen36-mi250-tracelab-20261107_amd" / "libmoe_probe.so"
+    if not path.exists():
+        pytest.skip("libmoe_probe.so not built (run __graft_entry__.build())")
+    lib = ctypes.CDLL(str(path))
+    fn = lib.moe_probe_stream_read
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_longlong, ctypes.c_void_p, ctypes.c_int,
+                   ctypes.c_void_p]
+    assert fn(None, 16, None, 1, None) == 1
+    assert fn(ctypes.c_void_p(16), 15, ctypes.c_void_p(16), 1, None) == 1
