@@ -23,15 +23,6 @@ __device__ __forceinline__ u32x4v lds_read_frag(uint32_t addr) {
   asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
   return r;
 }
-// 8 bytes from LDS byte address addr + OFF (completes at lds_frags_ready).
-typedef unsigned u32x2v __attribute__((ext_vector_type(2)));
-template <int OFF>
-__device__ __forceinline__ u32x2v lds_read_frag8(uint32_t addr) {
-  u32x2v r;
-  asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
-  return r;
-}
-__device__ __forceinline__ void after_wait(u32x2v& v) { asm volatile("" : "+v"(v)); }
 __device__ __forceinline__ void lds_frags_ready() {
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 }
