@@ -639,6 +639,13 @@ __global__ __launch_bounds__(1024) void k_dec_down1(DecodeArgs a) {
   const int I = IC * 512;
   const int H = a.H;
   const bool is_shared = wave == a.k;
+  // the combine's other inputs (shared-expert gate logit, residual) requested up front, so
+  // that no load waits after the barrier
+  float seg_in = 0.f, res_in = 0.f;
+  if (wave == 0 && lane < kDownRows) {
+    if (a.sh_down) seg_in = bf_bits2f(a.logits[a.E]);
+    if (a.residual) res_in = bf_bits2f(a.residual[n0 + lane]);
+  }
   if (is_shared && a.sh_down) {
     // the shared expert: no routing dependency
     uint4 xs[2], ws[kDownRows][2];
@@ -695,10 +702,10 @@ __global__ __launch_bounds__(1024) void k_dec_down1(DecodeArgs a) {
     for (int j = 0; j < a.k; ++j) acc += s_term[j][lane];  // routing order j
     float o = rbf(acc);
     if (a.sh_down) {
-      const float gte = rbf(sigmoidf_(bf_bits2f(a.logits[a.E])));
+      const float gte = rbf(sigmoidf_(seg_in));
       o = rbf(o + rbf(gte * s_term[15][lane]));
     }
-    if (a.residual) o += bf_bits2f(a.residual[n]);
+    if (a.residual) o += res_in;
     a.out[n] = f2bf_bits(o);
   }
 }
