@@ -98,7 +98,8 @@ def test_route_bruteforce_small(pkg, dev):
 
 
 SORT_CASES = [(1, 256, 8), (4, 16, 4), (64, 256, 8), (75, 16, 4), (300, 16, 4), (513, 256, 8),
-              (1000, 256, 8), (2049, 64, 2), (700, 512, 8), (4096, 256, 8)]
+              (1000, 256, 8), (2049, 64, 2), (700, 512, 8), (4096, 256, 8),
+              (5000, 256, 8)]  # 40000 pairs: more than 32 count blocks (the scan's other branch)
 
 
 @pytest.mark.parametrize("T,E,k", SORT_CASES)

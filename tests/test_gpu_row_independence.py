@@ -41,7 +41,7 @@ def mlp(dev):
                                               (1536, 1024, False),
                                               (4096, 2048, False), (1100, 900, False),
                                               (800, 700, False), (1024, 600, False),
-                                              (2048, 100, False)])
+                                              (2048, 100, False), (8192, 4096, False)])
 def test_leading_rows_match_smaller_batch(pkg, dev, mlp, big, small, decode):
     print(f"row independence {big} -> {small} decode={decode}", flush=True)
     g = torch.Generator().manual_seed(big + small)
